@@ -1,0 +1,328 @@
+/*
+ * rmda_moe.h - C ABI of the MI355X (gfx950) MoE feed-forward path.
+ *
+ * This library replaces the Vulkan dispatch of R-MDA's MoE teacher layer
+ * (reference: src/qwen.c:770-907 issuing mda_vkc_run, src/vkc.c:771-789) with
+ * hand-written HIP kernels.  Every entry point is plain C: device pointers,
+ * sizes and the reference's own argument structs (field for field the
+ * push-constant structs of src/pc.h), no C++ or torch types.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (hipMalloc'd or equivalent) unless stated.
+ *   - Calls are enqueue-only on the context's stream; nothing reads results
+ *     back to the host, so no device->host synchronisation happens inside a
+ *     call (the reference's layer is one GPU-resident command buffer,
+ *     src/qwen.c:1074-1076).  rmda_moe_sync() is the "flush".
+ *   - Return value: RMDA_OK (0) or a negative RMDA_ERR_* code.  The first
+ *     failure is also kept as a sticky error in the context and every later
+ *     call returns RMDA_ERR_STICKY without enqueueing work, mirroring the
+ *     reference's sticky c->fail (src/vkc.c:15-20, :771-789).  Nothing calls
+ *     exit().
+ *   - One context = one host thread at a time (the reference records from a
+ *     single thread, src/qwen.c:1069-1078).
+ *   - Hot calls never allocate device memory.  The context owns a small
+ *     fixed-capacity scratch area allocated once in rmda_moe_ctx_create();
+ *     the fused layer uses a caller-provided workspace.
+ */
+#ifndef RMDA_MOE_H
+#define RMDA_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same value as MDA_PC_NO_SLOT (src/pc.h:6): "no fp16 scale slot". */
+#define RMDA_NO_SLOT 0xffffffffu
+/* Sentinel for an unused tile / a pair with no selectable expert. */
+#define RMDA_NONE 0xffffffffu
+
+/* Reference limits kept by the drop-in kernels. */
+#define RMDA_MAX_EXPERTS 512u /* moe_scan runs 512 lanes, shader/moe_scan.comp:2 */
+#define RMDA_MAX_TOPK 16u     /* MAXK, shader/moe_route.comp:18 */
+#define RMDA_MM_TILE 128u     /* TILE, shader/matmul_f16_moe.comp:16; MDA_QWEN_TILE src/qwen.h:14 */
+
+/* Scratch capacity of a context: routed pairs (rows * topk) per call of
+ * rmda_moe_scatter.  Larger calls fail with RMDA_ERR_CAPACITY. */
+#define RMDA_CTX_MAX_PAIRS (1u << 21)
+
+enum {
+    RMDA_OK = 0,
+    RMDA_ERR_ARG = -1,       /* null pointer or invalid flag */
+    RMDA_ERR_SHAPE = -2,     /* shape violates a kernel's requirement */
+    RMDA_ERR_CAPACITY = -3,  /* beyond a documented maximum */
+    RMDA_ERR_HIP = -4,       /* a HIP runtime call failed */
+    RMDA_ERR_STICKY = -5,    /* an earlier call failed; context is poisoned */
+    RMDA_ERR_WORKSPACE = -6, /* caller workspace missing or too small */
+    RMDA_ERR_DEVICE = -7     /* no usable gfx950 device */
+};
+
+/* ---- argument structs: identical layout to the reference push constants ---- */
+
+/* src/pc.h:369-374 */
+typedef struct rmda_pc_moe_route_t {
+    uint32_t rows;
+    uint32_t experts;
+    uint32_t topk;
+    uint32_t stride;
+} rmda_pc_moe_route_t;
+
+/* src/pc.h:376-379 */
+typedef struct rmda_pc_moe_scan_t {
+    uint32_t experts;
+    uint32_t tile;
+} rmda_pc_moe_scan_t;
+
+/* src/pc.h:381-385 */
+typedef struct rmda_pc_moe_scatter_t {
+    uint32_t rows;
+    uint32_t topk;
+    uint32_t d8;
+} rmda_pc_moe_scatter_t;
+
+/* src/pc.h:387-393 */
+typedef struct rmda_pc_moe_mm_t {
+    uint32_t m;
+    uint32_t n;
+    uint32_t k;
+    uint32_t sa;
+    uint32_t sb;
+} rmda_pc_moe_mm_t;
+
+/* src/pc.h:395-404 */
+typedef struct rmda_pc_moe_combine_t {
+    uint32_t rows;
+    uint32_t d;
+    uint32_t topk;
+    uint32_t pstride;
+    uint32_t sg_off;
+    uint32_t inj_stride;
+    uint32_t inj_off;
+    uint32_t hc;
+} rmda_pc_moe_combine_t;
+
+/* src/pc.h:315-323 */
+typedef struct rmda_pc_qwen_elem_t {
+    uint32_t rows;
+    uint32_t n;
+    uint32_t astride;
+    uint32_t ao;
+    uint32_t bo;
+    uint32_t op;
+    float scale;
+} rmda_pc_qwen_elem_t;
+
+/* src/pc.h:85-88 */
+typedef struct rmda_pc_absmax_t {
+    uint32_t n;
+    uint32_t slot;
+} rmda_pc_absmax_t;
+
+/* src/pc.h:90-93 */
+typedef struct rmda_pc_cast_t {
+    uint32_t n;
+    uint32_t slot;
+} rmda_pc_cast_t;
+
+/* shader/qwen_bf16.comp:5-7 */
+typedef struct rmda_pc_qwen_bf16_t {
+    uint32_t n;
+} rmda_pc_qwen_bf16_t;
+
+/* ---- context ---- */
+
+typedef struct rmda_moe_ctx rmda_moe_ctx_t;
+
+/* Create a context on HIP device `device` issuing work on `stream`
+ * (a hipStream_t; NULL = the device's null stream).  Allocates the context's
+ * fixed scratch.  Fails with RMDA_ERR_DEVICE unless the device is gfx950. */
+int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream);
+void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx);
+int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream);
+/* Sticky error: RMDA_OK or the first failure's code, with a message. */
+int rmda_moe_ctx_error(const rmda_moe_ctx_t *ctx);
+const char *rmda_moe_ctx_message(const rmda_moe_ctx_t *ctx);
+void rmda_moe_ctx_clear_error(rmda_moe_ctx_t *ctx);
+/* Wait for all enqueued work: the replacement of mda_vkc_flush
+ * (src/vkc.c:655-668).  Reports asynchronous HIP errors. */
+int rmda_moe_sync(rmda_moe_ctx_t *ctx);
+/* Library version string and the gfx target it was built for. */
+const char *rmda_moe_version(void);
+
+/* ---- per-stage drop-ins (one per reference kernel, buffers in binding order) ---- */
+
+/* moe_route (shader/moe_route.comp; dispatched at src/qwen.c:799-811).
+ * For each row r: top `topk` of proj[r*stride + 0..experts) by value,
+ * descending, ties to the lower expert index, NaN and values <= -3e38 never
+ * selected; idx[r*topk+j] = expert, wt[r*topk+j] = exp(l_j - l_0) / sum_j.
+ * count[e] = number of (r, j) that selected e.  Unlike the reference, count is
+ * overwritten (the reference adds into a buffer the host zero-filled first,
+ * src/qwen.c:794).  A pair with no selectable expert gets idx RMDA_NONE and is
+ * not counted (the reference indexes count[~0u] there).
+ * Requires experts <= 512, 1 <= topk <= min(16, experts), stride >= experts. */
+int rmda_moe_route(rmda_moe_ctx_t *ctx, const rmda_pc_moe_route_t *pc,
+                   const float *proj, uint32_t *idx, float *wt, uint32_t *count);
+
+/* moe_scan (shader/moe_scan.comp; src/qwen.c:812-821).
+ * off[e] = sum_{e'<e} ceil(count[e']/tile)*tile; tiles[t] = e for each of
+ * expert e's tiles and RMDA_NONE for every other t < n_tiles (the reference
+ * relies on a host fill for those, src/qwen.c:796; n_tiles is that fill's
+ * length, mrows/tile).  Requires experts <= 512, tile >= 1. */
+int rmda_moe_scan(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scan_t *pc,
+                  const uint32_t *count, uint32_t *off, uint32_t *tiles, uint32_t n_tiles);
+
+/* moe_scatter (shader/moe_scatter.comp; src/qwen.c:822-835).
+ * slot[pr] = off[e] + (number of pr' < pr with idx[pr'] == e), e = idx[pr]:
+ * the stable order the reference's atomic counter produces when run
+ * sequentially, here produced deterministically.  Row pr/topk of x16
+ * (d8 16-byte chunks) is copied bitwise to row slot[pr] of xp.  Pairs with
+ * idx RMDA_NONE get slot RMDA_NONE and copy nothing.  `fill` is scratch of
+ * `experts` words: treated as zero on entry, left holding the per-expert
+ * counts (what the reference's atomics leave there).  Rows of xp that no pair
+ * targets are not written (the reference zero-fills them first,
+ * src/qwen.c:798; rmda_moe_mm never reads them as valid data).
+ * `experts` is taken from the context's last rmda_moe_route call unless set
+ * with rmda_moe_scatter_experts().  Requires rows*topk <= RMDA_CTX_MAX_PAIRS. */
+int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc,
+                     const uint32_t *idx, const uint32_t *off, uint32_t *fill,
+                     const uint16_t *x16, uint16_t *xp, uint32_t *slot);
+int rmda_moe_scatter_experts(rmda_moe_ctx_t *ctx, uint32_t experts);
+
+/* matmul_f16_moe (shader/matmul_f16_moe.comp; src/qwen.c:770-786).
+ * For each 128-row tile t of A with e = tiles[t] != RMDA_NONE:
+ * C[r, 0..n) = (A[r, :] . B[e][0..n)[:]) / (scale(sa) * scale(sb)) for the
+ * 128 rows r of the tile; fp16 inputs, fp32 accumulate, fp32 output.
+ * B is [experts][n][k] fp16 (HF [out, in] per expert).  Rows of tiles marked
+ * RMDA_NONE are not written.  amax holds the fp16 scale slots (may be NULL if
+ * sa == sb == RMDA_NO_SLOT).  Requires m % 128 == 0, n % 128 == 0,
+ * k % 32 == 0 (the reference's grid and K-step). */
+int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc,
+                const uint16_t *a, const uint16_t *b, float *c,
+                const uint32_t *amax, const uint32_t *tiles);
+
+/* moe_combine (shader/moe_combine.comp; src/qwen.c:887-906).
+ * acc[r,c] = sum_j wt[r,j] * y[slot[r,j], c]
+ *          + sigmoid(proj[r*pstride + sg_off]) * sh[r*d + c];
+ * h[r, s, c] += acc * 2 * sigmoid(inj[r*inj_stride + inj_off + s] / hc), s < hc.
+ * Extension: sh == NULL drops the shared-expert term (proj unused then);
+ * pairs with slot RMDA_NONE contribute nothing. */
+int rmda_moe_combine(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc,
+                     const float *wt, const uint32_t *slot, const float *y,
+                     const float *proj, const float *sh, const float *inj, float *h);
+
+/* Plain-output combine (no hyper-connection streams): out[r,c] = acc as fp16.
+ * Same acc as rmda_moe_combine. */
+int rmda_moe_combine_plain(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc,
+                           const float *wt, const uint32_t *slot, const float *y,
+                           const float *proj, const float *sh, uint16_t *out);
+
+/* qwen_elem (shader/qwen_elem.comp; used at src/qwen.c:848-857, :879-884).
+ * op 0: y[r*n+c] = silu(a[r*astride+ao+c]) * a[r*astride+bo+c];
+ * op 1: y[r*n+c] = silu(a[r*astride+ao+c] * scale); silu(v) = v/(1+exp(-v)). */
+int rmda_qwen_elem(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_elem_t *pc,
+                   const float *a, float *y);
+
+/* absmax (shader/absmax.comp): amax[slot] = max(amax[slot], max_i |x[i]|) on
+ * the float bit patterns (values are non-negative). */
+int rmda_absmax(rmda_moe_ctx_t *ctx, const rmda_pc_absmax_t *pc,
+                const float *x, uint32_t *amax);
+
+/* cast_f16 (shader/cast_f16.comp): dst[i] = fp16(src[i] * scale(slot)),
+ * scale = 2^(141 - biased_exponent(amax[slot])), 1 for RMDA_NO_SLOT or a
+ * zero / non-finite amax.  Round to nearest even. */
+int rmda_cast_f16(rmda_moe_ctx_t *ctx, const rmda_pc_cast_t *pc,
+                  const float *src, uint16_t *dst, const uint32_t *amax);
+
+/* qwen_bf16 (shader/qwen_bf16.comp; src/qwen.c:386-390): in place, each
+ * 32-bit word holding two bf16 becomes two fp16 (round to nearest even). */
+int rmda_qwen_bf16(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_bf16_t *pc, uint32_t *w);
+
+/* ---- router projection (replaces the dense fp16 GEMM into `p`, src/qwen.c:845) ---- */
+
+/* proj[r*stride + c] = x16[r, :] . w[c, :] for c < cols, plus bias[c] for
+ * c < nbias when bias != NULL.  x16 is rows x d fp16, w is cols x d fp32
+ * (HF [out, in]: rows 0..E-1 the router, row E the shared-expert gate when
+ * present, as in the reference's packed p layout, src/qwen.c:444-449).
+ * fp32 arithmetic in one fixed order that the CPU oracle replays exactly:
+ * d is cut into 8 contiguous chunks; each chunk is a sequential fmaf chain
+ * from 0; the chunk sums are added left to right; then the bias.
+ * Requires d % 32 == 0, stride >= cols, cols <= 1024. */
+typedef struct rmda_moe_router_t {
+    uint32_t rows;
+    uint32_t d;
+    uint32_t cols;
+    uint32_t stride;
+    uint32_t nbias;
+} rmda_moe_router_t;
+
+int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc,
+                    const uint16_t *x16, const float *w, const float *bias, float *proj);
+
+/* ---- fused MoE layer (replaces mda_qwen_moe_rec, src/qwen.c:838-907) ---- */
+
+typedef struct rmda_moe_shape_t {
+    uint32_t rows;    /* tokens T in this call */
+    uint32_t d;       /* hidden size */
+    uint32_t experts; /* routed experts E */
+    uint32_t topk;    /* k */
+    uint32_t inter;   /* routed expert intermediate size I */
+    uint32_t shared;  /* shared expert intermediate size I_s, 0 = none */
+} rmda_moe_shape_t;
+
+typedef struct rmda_moe_layer_args_t {
+    const uint16_t *x;          /* rows x d fp16 activations */
+    const float *w_router;      /* (experts [+1 shared gate]) x d fp32 */
+    const float *bias;          /* experts fp32 router bias, or NULL */
+    const uint16_t *w_gate_up;  /* [experts][2*inter][d] fp16: gate rows then up rows */
+    const uint16_t *w_down;     /* [experts][d][inter] fp16 */
+    const uint16_t *w_sh_gate_up; /* [2*shared][d] fp16 or NULL when shared == 0 */
+    const uint16_t *w_sh_down;    /* [d][shared] fp16 or NULL when shared == 0 */
+    uint16_t *out;              /* rows x d fp16 */
+    void *workspace;            /* >= rmda_moe_workspace_bytes(shape) bytes */
+    size_t workspace_bytes;
+} rmda_moe_layer_args_t;
+
+/* Device views into the workspace after rmda_moe_layer (byte offsets), so a
+ * caller can inspect routing: proj [rows][proj_stride] fp32, idx/wt/slot
+ * [rows*topk], count/off [experts]. */
+typedef struct rmda_moe_ws_layout_t {
+    size_t proj;
+    size_t idx;
+    size_t wt;
+    size_t count;
+    size_t off;
+    size_t slot;
+    size_t total;
+    uint32_t proj_stride;
+} rmda_moe_ws_layout_t;
+
+size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape);
+int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_t *out);
+
+/* The whole layer: router -> route -> scan -> permutation -> grouped SwiGLU
+ * gate_up GEMM -> grouped down GEMM -> (shared expert) -> combine, enqueued on
+ * the context stream with no host synchronisation.
+ * out[r] = sum_j wt[r,j] * FFN_{idx[r,j]}(x[r]) (+ sigmoid(g_r) * FFN_shared(x[r])).
+ * Expert segments are packed without padding (tile 1); the permutation is
+ * the stable order of rmda_moe_scatter.  Requires d % 256 == 0,
+ * inter % 64 == 0, shared % 64 == 0, experts <= 512, topk <= 16. */
+int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
+                   const rmda_moe_layer_args_t *args);
+
+/* ---- synthetic inputs (bench and tests) ---- */
+
+/* dst[i] = fp16 / fp32 of std * z_i where z_i is the standardised
+ * Irwin-Hall(4) variate of counter hash (stream, seed, i): exact integer and
+ * IEEE float steps only, so any host reproduces it bit for bit. */
+int rmda_moe_fill_normal_f16(rmda_moe_ctx_t *ctx, uint16_t *dst, size_t n,
+                             uint64_t stream, uint64_t seed, float std);
+int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n,
+                             uint64_t stream, uint64_t seed, float std);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

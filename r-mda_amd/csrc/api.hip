@@ -1,0 +1,658 @@
+// C ABI of the MoE path: context, sticky errors, argument checks, the
+// per-stage drop-ins and the fused layer driver.  Replaces, for this path
+// only, the reference's Vulkan dispatch (mda_vkc_run, src/vkc.c:771-789) and
+// the recording in mda_qwen_moe_rec / mda_qwen_route_rec / mda_qwen_moe_mm
+// (src/qwen.c:770-907).  Every call only enqueues work on the context stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+struct rmda_moe_ctx {
+    int device;
+    hipStream_t stream;
+    int err;
+    char msg[256];
+    // fixed scratch for rmda_moe_scatter (allocated once at creation)
+    uint32_t *scratch;
+    uint32_t *lrank;
+    uint32_t *hist;
+    uint32_t *done;
+    uint32_t scatter_experts;
+};
+
+namespace {
+
+constexpr size_t kHistBlocks = (RMDA_CTX_MAX_PAIRS + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
+
+int fail(rmda_moe_ctx_t *c, int code, const char *fmt, ...) {
+    if (c != nullptr && c->err == RMDA_OK) {
+        c->err = code;
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(c->msg, sizeof(c->msg), fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+// Entry guard: null context, sticky error, and the context's device current.
+int enter(rmda_moe_ctx_t *c) {
+    if (c == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    if (c->err != RMDA_OK) {
+        return RMDA_ERR_STICKY;
+    }
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != c->device) {
+        if (hipSetDevice(c->device) != hipSuccess) {
+            return fail(c, RMDA_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+        }
+    }
+    return RMDA_OK;
+}
+
+int hip_check(rmda_moe_ctx_t *c, hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        return fail(c, RMDA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    return RMDA_OK;
+}
+
+size_t align256(size_t x) {
+    return (x + 255) & ~(size_t)255;
+}
+
+struct LayerPlan {
+    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, items, hp, ye, total;
+    uint32_t ps, npairs, nblocks, max_items, sh_rows, groups_rows;
+};
+
+int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
+    if (s->d == 0 || s->d % 128 != 0) {
+        snprintf(why, n, "d=%u must be a positive multiple of 128", s->d);
+        return 0;
+    }
+    if (s->experts == 0 || s->experts > RMDA_MAX_EXPERTS) {
+        snprintf(why, n, "experts=%u must be in 1..%u", s->experts, RMDA_MAX_EXPERTS);
+        return 0;
+    }
+    if (s->topk == 0 || s->topk > RMDA_MAX_TOPK || s->topk > s->experts) {
+        snprintf(why, n, "topk=%u must be in 1..min(%u, experts)", s->topk, RMDA_MAX_TOPK);
+        return 0;
+    }
+    if (s->inter == 0 || s->inter % 64 != 0) {
+        snprintf(why, n, "inter=%u must be a positive multiple of 64", s->inter);
+        return 0;
+    }
+    if (s->shared != 0 && s->shared != s->inter) {
+        snprintf(why, n, "shared=%u must be 0 or equal to inter=%u", s->shared, s->inter);
+        return 0;
+    }
+    if ((uint64_t)s->rows * s->topk + s->rows >= (1ull << 31)) {
+        snprintf(why, n, "rows*topk too large");
+        return 0;
+    }
+    return 1;
+}
+
+LayerPlan plan_layer(const rmda_moe_shape_t *s) {
+    LayerPlan p{};
+    const uint32_t T = s->rows;
+    const uint32_t K = s->topk;
+    const uint32_t E = s->experts;
+    p.ps = E + (s->shared > 0 ? 1u : 0u);
+    p.npairs = T * K;
+    p.nblocks = p.npairs == 0 ? 1 : (p.npairs + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
+    p.sh_rows = s->shared > 0 ? T : 0;
+    p.max_items = p.npairs / RMDA_GEMM_BM + E + (p.sh_rows + RMDA_GEMM_BM - 1) / RMDA_GEMM_BM;
+    p.groups_rows = p.npairs + p.sh_rows;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    p.proj = take((size_t)T * p.ps * 4);
+    p.idx = take((size_t)p.npairs * 4);
+    p.wt = take((size_t)p.npairs * 4);
+    p.lrank = take((size_t)p.npairs * 4);
+    p.slot = take((size_t)p.npairs * 4);
+    p.rowtok = take((size_t)p.npairs * 4);
+    p.count = take((size_t)E * 4);
+    p.off = take((size_t)E * 4);
+    p.hist = take((size_t)p.nblocks * E * 4);
+    p.done = take(4);
+    p.n_items = take(4);
+    p.items = take((size_t)p.max_items * 16);
+    p.hp = take((size_t)p.groups_rows * s->inter * 2);
+    p.ye = take((size_t)p.groups_rows * s->d * 2);
+    p.total = o;
+    return p;
+}
+
+template <typename T>
+T *at(void *base, size_t off) {
+    return reinterpret_cast<T *>(reinterpret_cast<char *>(base) + off);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *rmda_moe_version(void) {
+    return "rmda_moe 0.1 (gfx950, wave64, fp16 MFMA)";
+}
+
+int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
+    if (out == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        return RMDA_ERR_DEVICE;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        return RMDA_ERR_DEVICE;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return RMDA_ERR_DEVICE;
+    }
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    if (hipSetDevice(device) != hipSuccess) {
+        return RMDA_ERR_DEVICE;
+    }
+    rmda_moe_ctx_t *c = new rmda_moe_ctx_t();
+    c->device = device;
+    c->stream = reinterpret_cast<hipStream_t>(stream);
+    c->err = RMDA_OK;
+    c->msg[0] = 0;
+    const size_t words = (size_t)RMDA_CTX_MAX_PAIRS + kHistBlocks * RMDA_MAX_EXPERTS + 64;
+    if (hipMalloc(&c->scratch, words * 4) != hipSuccess) {
+        delete c;
+        return RMDA_ERR_HIP;
+    }
+    c->lrank = c->scratch;
+    c->hist = c->lrank + RMDA_CTX_MAX_PAIRS;
+    c->done = c->hist + kHistBlocks * RMDA_MAX_EXPERTS;
+    // the rank ticket must start at zero; the kernel leaves it at zero
+    if (hipMemset(c->done, 0, 64 * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(c->scratch);
+        delete c;
+        return RMDA_ERR_HIP;
+    }
+    c->scatter_experts = 0;
+    if (prev >= 0 && prev != device) {
+        (void)hipSetDevice(prev);
+    }
+    *out = c;
+    return RMDA_OK;
+}
+
+void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
+    if (ctx == nullptr) {
+        return;
+    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(ctx->scratch);
+    delete ctx;
+}
+
+int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream) {
+    if (ctx == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    ctx->stream = reinterpret_cast<hipStream_t>(stream);
+    return RMDA_OK;
+}
+
+int rmda_moe_ctx_error(const rmda_moe_ctx_t *ctx) {
+    return ctx == nullptr ? RMDA_ERR_ARG : ctx->err;
+}
+
+const char *rmda_moe_ctx_message(const rmda_moe_ctx_t *ctx) {
+    return ctx == nullptr ? "null context" : ctx->msg;
+}
+
+void rmda_moe_ctx_clear_error(rmda_moe_ctx_t *ctx) {
+    if (ctx != nullptr) {
+        ctx->err = RMDA_OK;
+        ctx->msg[0] = 0;
+    }
+}
+
+int rmda_moe_sync(rmda_moe_ctx_t *ctx) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+// ---- per-stage drop-ins ----
+
+int rmda_moe_route(rmda_moe_ctx_t *ctx, const rmda_pc_moe_route_t *pc, const float *proj, uint32_t *idx,
+                   float *wt, uint32_t *count) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || proj == nullptr || idx == nullptr || wt == nullptr || count == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_route: null argument");
+    }
+    if (pc->experts == 0 || pc->experts > RMDA_MAX_EXPERTS) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_route: experts=%u not in 1..%u", pc->experts, RMDA_MAX_EXPERTS);
+    }
+    if (pc->topk == 0 || pc->topk > RMDA_MAX_TOPK || pc->topk > pc->experts) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_route: topk=%u not in 1..min(%u, experts)", pc->topk,
+                    RMDA_MAX_TOPK);
+    }
+    if (pc->stride < pc->experts) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_route: stride=%u < experts=%u", pc->stride, pc->experts);
+    }
+    rc = hip_check(ctx, rmda_launch_zero(ctx->stream, count, pc->experts, 0), "zero count");
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_route(ctx->stream, proj, idx, wt, count, pc->rows, pc->experts, pc->topk,
+                                              pc->stride),
+                       "route");
+    }
+    if (rc == RMDA_OK) {
+        ctx->scatter_experts = pc->experts;
+    }
+    return rc;
+}
+
+int rmda_moe_scan(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scan_t *pc, const uint32_t *count, uint32_t *off,
+                  uint32_t *tiles, uint32_t n_tiles) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || count == nullptr || off == nullptr || (tiles == nullptr && n_tiles > 0)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scan: null argument");
+    }
+    if (pc->experts == 0 || pc->experts > RMDA_MAX_EXPERTS || pc->tile == 0) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_scan: experts=%u tile=%u", pc->experts, pc->tile);
+    }
+    return hip_check(ctx, rmda_launch_scan(ctx->stream, count, off, tiles, n_tiles, pc->experts, pc->tile),
+                     "scan");
+}
+
+int rmda_moe_scatter_experts(rmda_moe_ctx_t *ctx, uint32_t experts) {
+    if (ctx == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    if (experts == 0 || experts > RMDA_MAX_EXPERTS) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_scatter_experts: experts=%u", experts);
+    }
+    ctx->scatter_experts = experts;
+    return RMDA_OK;
+}
+
+int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc, const uint32_t *idx,
+                     const uint32_t *off, uint32_t *fill, const uint16_t *x16, uint16_t *xp, uint32_t *slot) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || idx == nullptr || off == nullptr || fill == nullptr || slot == nullptr ||
+        (xp != nullptr && x16 == nullptr)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scatter: null argument");
+    }
+    if (ctx->scatter_experts == 0) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scatter: expert count unknown (call rmda_moe_route or "
+                                       "rmda_moe_scatter_experts first)");
+    }
+    const uint64_t npairs = (uint64_t)pc->rows * pc->topk;
+    if (npairs > RMDA_CTX_MAX_PAIRS) {
+        return fail(ctx, RMDA_ERR_CAPACITY, "rmda_moe_scatter: rows*topk=%llu exceeds %u",
+                    (unsigned long long)npairs, RMDA_CTX_MAX_PAIRS);
+    }
+    if (pc->topk == 0 || pc->topk > RMDA_MAX_TOPK || (xp != nullptr && pc->d8 == 0)) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_scatter: topk=%u d8=%u", pc->topk, pc->d8);
+    }
+    rmda_rank_args_t ra{};
+    ra.idx = idx;
+    ra.npairs = (uint32_t)npairs;
+    ra.experts = ctx->scatter_experts;
+    ra.tile = 1;
+    ra.lrank = ctx->lrank;
+    ra.hist = ctx->hist;
+    ra.count = fill;  // the reference's atomics leave the per-expert counts in fill
+    ra.off = nullptr;
+    ra.off_in = off;
+    ra.done = ctx->done;
+    rc = hip_check(ctx, rmda_launch_rank(ctx->stream, &ra), "rank");
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    return hip_check(ctx, rmda_launch_permute(ctx->stream, idx, ctx->lrank, ctx->hist, (uint32_t)npairs, pc->topk,
+                                              ctx->scatter_experts, slot, nullptr, x16, xp, pc->d8),
+                     "permute");
+}
+
+int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t *a, const uint16_t *b, float *c,
+                const uint32_t *amax, const uint32_t *tiles) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || a == nullptr || b == nullptr || c == nullptr || tiles == nullptr ||
+        (amax == nullptr && (pc->sa != RMDA_NO_SLOT || pc->sb != RMDA_NO_SLOT))) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_mm: null argument");
+    }
+    if (pc->m % RMDA_MM_TILE != 0 || pc->n == 0 || pc->n % RMDA_MM_TILE != 0 || pc->k == 0 || pc->k % 32 != 0) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_mm: m=%u n=%u k=%u (need m,n %% 128 == 0, k %% 32 == 0)", pc->m,
+                    pc->n, pc->k);
+    }
+    rmda_gemm_args_t g{};
+    g.mode = RMDA_GEMM_F32;
+    g.a = a;
+    g.lda = pc->k;
+    g.w = b;
+    g.shared_group = RMDA_NONE;
+    g.n_w = pc->n;
+    g.k = pc->k;
+    g.n_out = pc->n;
+    g.out = c;
+    g.ldo = pc->n;
+    g.max_items = pc->m / RMDA_MM_TILE;
+    g.tiles = tiles;
+    g.amax = amax;
+    g.sa = pc->sa;
+    g.sb = pc->sb;
+    return hip_check(ctx, rmda_launch_gemm(ctx->stream, &g), "moe_mm");
+}
+
+static int combine_common(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc, const float *wt,
+                          const uint32_t *slot, const float *y, const float *proj, const float *sh,
+                          const float *inj, float *h, uint16_t *out) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || wt == nullptr || slot == nullptr || y == nullptr || (sh != nullptr && proj == nullptr) ||
+        (out == nullptr && pc->hc > 0 && (inj == nullptr || h == nullptr))) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_combine: null argument");
+    }
+    if (pc->topk == 0 || pc->topk > RMDA_MAX_TOPK) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_combine: topk=%u", pc->topk);
+    }
+    return hip_check(ctx, rmda_launch_combine(ctx->stream, pc, wt, slot, y, proj, sh, inj, h, out), "combine");
+}
+
+int rmda_moe_combine(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc, const float *wt, const uint32_t *slot,
+                     const float *y, const float *proj, const float *sh, const float *inj, float *h) {
+    return combine_common(ctx, pc, wt, slot, y, proj, sh, inj, h, nullptr);
+}
+
+int rmda_moe_combine_plain(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc, const float *wt,
+                           const uint32_t *slot, const float *y, const float *proj, const float *sh,
+                           uint16_t *out) {
+    if (out == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_combine_plain: null out");
+    }
+    return combine_common(ctx, pc, wt, slot, y, proj, sh, nullptr, nullptr, out);
+}
+
+int rmda_qwen_elem(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_elem_t *pc, const float *a, float *y) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || a == nullptr || y == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_qwen_elem: null argument");
+    }
+    if (pc->op > 1) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_qwen_elem: op=%u", pc->op);
+    }
+    return hip_check(ctx, rmda_launch_elem(ctx->stream, pc, a, y), "qwen_elem");
+}
+
+int rmda_absmax(rmda_moe_ctx_t *ctx, const rmda_pc_absmax_t *pc, const float *x, uint32_t *amax) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || x == nullptr || amax == nullptr || pc->slot == RMDA_NO_SLOT) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_absmax: null argument or no slot");
+    }
+    return hip_check(ctx, rmda_launch_absmax(ctx->stream, pc, x, amax), "absmax");
+}
+
+int rmda_cast_f16(rmda_moe_ctx_t *ctx, const rmda_pc_cast_t *pc, const float *src, uint16_t *dst,
+                  const uint32_t *amax) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || src == nullptr || dst == nullptr || (amax == nullptr && pc->slot != RMDA_NO_SLOT)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_cast_f16: null argument");
+    }
+    return hip_check(ctx, rmda_launch_cast(ctx->stream, pc, src, dst, amax), "cast_f16");
+}
+
+int rmda_qwen_bf16(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_bf16_t *pc, uint32_t *w) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || w == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_qwen_bf16: null argument");
+    }
+    return hip_check(ctx, rmda_launch_bf16(ctx->stream, pc->n, w), "qwen_bf16");
+}
+
+int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
+                    const float *bias, float *proj) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (pc == nullptr || x16 == nullptr || w == nullptr || proj == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_router: null argument");
+    }
+    if (pc->d == 0 || pc->d % 128 != 0 || pc->cols == 0 || pc->cols > 65536 || pc->stride < pc->cols) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_router: d=%u cols=%u stride=%u (need d %% 128 == 0, "
+                                         "1 <= cols <= stride)",
+                    pc->d, pc->cols, pc->stride);
+    }
+    if (pc->rows == 0) {
+        return RMDA_OK;
+    }
+    return hip_check(ctx, rmda_launch_router(ctx->stream, x16, w, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
+                                             bias != nullptr ? pc->nbias : 0, nullptr, 0),
+                     "router");
+}
+
+// ---- fused layer ----
+
+size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape) {
+    if (shape == nullptr) {
+        return 0;
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return 0;
+    }
+    return plan_layer(shape).total;
+}
+
+int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_t *out) {
+    if (shape == nullptr || out == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return RMDA_ERR_SHAPE;
+    }
+    const LayerPlan p = plan_layer(shape);
+    out->proj = p.proj;
+    out->idx = p.idx;
+    out->wt = p.wt;
+    out->count = p.count;
+    out->off = p.off;
+    out->slot = p.slot;
+    out->total = p.total;
+    out->proj_stride = p.ps;
+    return RMDA_OK;
+}
+
+int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmda_moe_layer_args_t *args) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (shape == nullptr || args == nullptr || args->x == nullptr || args->w_router == nullptr ||
+        args->w_gate_up == nullptr || args->w_down == nullptr || args->out == nullptr ||
+        args->workspace == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: null argument");
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_layer: %s", why);
+    }
+    if (shape->shared > 0 && (args->w_sh_gate_up == nullptr || args->w_sh_down == nullptr)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: shared expert weights missing");
+    }
+    const LayerPlan p = plan_layer(shape);
+    if (args->workspace_bytes < p.total) {
+        return fail(ctx, RMDA_ERR_WORKSPACE, "rmda_moe_layer: workspace %zu bytes < %zu", args->workspace_bytes,
+                    p.total);
+    }
+    if (shape->rows == 0) {
+        return RMDA_OK;
+    }
+    void *ws = args->workspace;
+    const uint32_t T = shape->rows;
+    const uint32_t E = shape->experts;
+    const uint32_t K = shape->topk;
+    const uint32_t I = shape->inter;
+    const uint32_t d = shape->d;
+    hipStream_t s = ctx->stream;
+    float *proj = at<float>(ws, p.proj);
+    uint32_t *idx = at<uint32_t>(ws, p.idx);
+    float *wt = at<float>(ws, p.wt);
+    uint32_t *lrank = at<uint32_t>(ws, p.lrank);
+    uint32_t *slot = at<uint32_t>(ws, p.slot);
+    uint32_t *rowtok = at<uint32_t>(ws, p.rowtok);
+    uint32_t *done = at<uint32_t>(ws, p.done);
+    uint16_t *hp = at<uint16_t>(ws, p.hp);
+    uint16_t *ye = at<uint16_t>(ws, p.ye);
+
+    // A0 router projection (+ zero the rank ticket for this call)
+    rc = hip_check(ctx,
+                   rmda_launch_router(s, args->x, args->w_router, args->bias, proj, T, d, p.ps, p.ps,
+                                      args->bias != nullptr ? E : 0, done, 1),
+                   "layer router");
+    // A1 top-k
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
+    }
+    // A2 counts, offsets, block bases and the GEMM work list
+    if (rc == RMDA_OK) {
+        rmda_rank_args_t ra{};
+        ra.idx = idx;
+        ra.npairs = p.npairs;
+        ra.experts = E;
+        ra.tile = 1;
+        ra.lrank = lrank;
+        ra.hist = at<uint32_t>(ws, p.hist);
+        ra.count = at<uint32_t>(ws, p.count);
+        ra.off = at<uint32_t>(ws, p.off);
+        ra.done = done;
+        ra.items = at<uint32_t>(ws, p.items);
+        ra.n_items = at<uint32_t>(ws, p.n_items);
+        ra.bm = RMDA_GEMM_BM;
+        ra.shared_rows = p.sh_rows;
+        ra.shared_row0 = p.npairs;
+        rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
+    }
+    // A3 permutation (slots + row -> token map; x is gathered, not copied)
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx,
+                       rmda_launch_permute(s, idx, lrank, at<uint32_t>(ws, p.hist), p.npairs, K, E, slot, rowtok,
+                                           nullptr, nullptr, 0),
+                       "layer permute");
+    }
+    rmda_gemm_args_t g{};
+    g.items = at<uint32_t>(ws, p.items);
+    g.n_items = at<uint32_t>(ws, p.n_items);
+    g.max_items = p.max_items;
+    g.shared_group = shape->shared > 0 ? E : RMDA_NONE;
+    g.shared_row0 = p.npairs;
+    g.sa = RMDA_NO_SLOT;
+    g.sb = RMDA_NO_SLOT;
+    // A4-A6 gate_up with SwiGLU epilogue -> hp16
+    if (rc == RMDA_OK) {
+        g.mode = RMDA_GEMM_SWIGLU;
+        g.a = args->x;
+        g.rowtok = rowtok;
+        g.lda = d;
+        g.w = args->w_gate_up;
+        g.w_shared = args->w_sh_gate_up;
+        g.n_w = 2 * I;
+        g.k = d;
+        g.n_out = I;
+        g.inter = I;
+        g.out = hp;
+        g.ldo = I;
+        rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer gate_up");
+    }
+    // A7 down -> ye16 (the shared expert's rows follow the routed rows)
+    if (rc == RMDA_OK) {
+        g.mode = RMDA_GEMM_F16;
+        g.a = hp;
+        g.rowtok = nullptr;
+        g.lda = I;
+        g.w = args->w_down;
+        g.w_shared = args->w_sh_down;
+        g.n_w = d;
+        g.k = I;
+        g.n_out = d;
+        g.inter = 0;
+        g.out = ye;
+        g.ldo = d;
+        rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer down");
+    }
+    // A8/A9 combine (+ sigmoid-gated shared expert)
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx,
+                       rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.npairs, shape->shared > 0, args->out,
+                                             T, d, K),
+                       "layer combine");
+    }
+    return rc;
+}
+
+int rmda_moe_fill_normal_f16(rmda_moe_ctx_t *ctx, uint16_t *dst, size_t n, uint64_t stream, uint64_t seed,
+                             float std) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (dst == nullptr && n > 0) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_fill_normal_f16: null dst");
+    }
+    return hip_check(ctx, rmda_launch_fill_normal(ctx->stream, dst, n, 1, stream, seed, std), "fill f16");
+}
+
+int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n, uint64_t stream, uint64_t seed,
+                             float std) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (dst == nullptr && n > 0) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_fill_normal_f32: null dst");
+    }
+    return hip_check(ctx, rmda_launch_fill_normal(ctx->stream, dst, n, 0, stream, seed, std), "fill f32");
+}
+
+}  // extern "C"

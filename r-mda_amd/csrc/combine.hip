@@ -1,0 +1,140 @@
+// Weighted gather-sum of expert outputs back to token order.
+//
+// combine_ref_kernel restates shader/moe_combine.comp:26-40 (fp32 expert
+// rows `y`, shared-expert term, hyper-connection streams h += acc * 2 *
+// sigmoid(inj / hc)), plus a plain fp16 output mode.  One thread per output
+// element, like the reference.
+//
+// combine16_kernel is the fused layer's version: fp16 expert rows, plain fp16
+// output, one workgroup per token.  The token's topk (slot, weight) pairs are
+// read once into LDS; each thread then handles 8 consecutive columns with
+// 16-byte loads of every selected row, accumulating in fp32 in j order (the
+// reference's order, :32-34) before the shared-expert term (:35).
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ float sigmoidf(float v) {
+    return 1.0f / (1.0f + expf(-v));
+}
+
+__global__ __launch_bounds__(256) void combine_ref_kernel(rmda_pc_moe_combine_t pc,
+                                                          const float *__restrict__ wt,
+                                                          const uint32_t *__restrict__ slot,
+                                                          const float *__restrict__ y,
+                                                          const float *__restrict__ proj,
+                                                          const float *__restrict__ sh,
+                                                          const float *__restrict__ inj,
+                                                          float *__restrict__ h,
+                                                          uint16_t *__restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)pc.rows * pc.d) {
+        return;
+    }
+    const uint32_t r = (uint32_t)(i / pc.d);
+    const uint32_t c = (uint32_t)(i % pc.d);
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < pc.topk; j += 1) {
+        const uint32_t s = slot[(size_t)r * pc.topk + j];
+        if (s != RMDA_NONE) {
+            acc += wt[(size_t)r * pc.topk + j] * y[(size_t)s * pc.d + c];
+        }
+    }
+    if (sh != nullptr) {
+        acc += sigmoidf(proj[(size_t)r * pc.pstride + pc.sg_off]) * sh[i];
+    }
+    if (out != nullptr) {
+        out[i] = rmda_f2h(acc);
+        return;
+    }
+    for (uint32_t s = 0; s < pc.hc; s += 1) {
+        const float gte = sigmoidf(inj[(size_t)r * pc.inj_stride + pc.inj_off + s] / (float)pc.hc);
+        h[(size_t)r * pc.hc * pc.d + (size_t)s * pc.d + c] += acc * 2.0f * gte;
+    }
+}
+
+__global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict__ wt,
+                                                        const uint32_t *__restrict__ slot,
+                                                        const uint16_t *__restrict__ y,
+                                                        const float *__restrict__ proj,
+                                                        uint32_t pstride, uint32_t sg_off,
+                                                        uint32_t shared_row0, int has_shared,
+                                                        uint16_t *__restrict__ out, uint32_t d,
+                                                        uint32_t topk) {
+    __shared__ uint32_t s_slot[RMDA_MAX_TOPK + 1];
+    __shared__ float s_wt[RMDA_MAX_TOPK + 1];
+    const uint32_t r = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    if (tid < topk) {
+        s_slot[tid] = slot[(size_t)r * topk + tid];
+        s_wt[tid] = wt[(size_t)r * topk + tid];
+    }
+    if (tid == 0 && has_shared) {
+        s_slot[RMDA_MAX_TOPK] = shared_row0 + r;
+        s_wt[RMDA_MAX_TOPK] = sigmoidf(proj[(size_t)r * pstride + sg_off]);
+    }
+    __syncthreads();
+    const uint32_t d8 = d / 8;
+    for (uint32_t c = tid; c < d8; c += 256) {
+        float acc[8];
+#pragma unroll
+        for (int v = 0; v < 8; v += 1) {
+            acc[v] = 0.0f;
+        }
+        for (uint32_t j = 0; j < topk; j += 1) {
+            const uint32_t s = s_slot[j];
+            if (s == RMDA_NONE) {
+                continue;
+            }
+            const float wj = s_wt[j];
+            const uint4 q = reinterpret_cast<const uint4 *>(y + (size_t)s * d)[c];
+            const uint16_t *hv = reinterpret_cast<const uint16_t *>(&q);
+#pragma unroll
+            for (int v = 0; v < 8; v += 1) {
+                acc[v] += wj * rmda_h2f(hv[v]);
+            }
+        }
+        if (has_shared) {
+            const float wj = s_wt[RMDA_MAX_TOPK];
+            const uint4 q = reinterpret_cast<const uint4 *>(y + (size_t)s_slot[RMDA_MAX_TOPK] * d)[c];
+            const uint16_t *hv = reinterpret_cast<const uint16_t *>(&q);
+#pragma unroll
+            for (int v = 0; v < 8; v += 1) {
+                acc[v] += wj * rmda_h2f(hv[v]);
+            }
+        }
+        uint4 o;
+        uint16_t *ov = reinterpret_cast<uint16_t *>(&o);
+#pragma unroll
+        for (int v = 0; v < 8; v += 1) {
+            ov[v] = rmda_f2h(acc[v]);
+        }
+        reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = o;
+    }
+}
+
+}  // namespace
+
+hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, const float *wt,
+                               const uint32_t *slot, const float *y, const float *proj,
+                               const float *sh, const float *inj, float *h, uint16_t *out) {
+    const uint64_t n = (uint64_t)pc->rows * pc->d;
+    if (n == 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(combine_ref_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, *pc, wt, slot,
+                       y, proj, sh, inj, h, out);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
+                                 const uint16_t *y, const float *proj, uint32_t pstride,
+                                 uint32_t sg_off, uint32_t shared_row0, int has_shared,
+                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk) {
+    if (rows == 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(combine16_kernel, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride, sg_off,
+                       shared_row0, has_shared, out, d, topk);
+    return hipGetLastError();
+}

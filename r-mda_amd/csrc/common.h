@@ -1,0 +1,144 @@
+// Shared device helpers and the launch interface between the C-ABI layer
+// (api.hip) and the kernel files.  gfx950 only: wave64, fp16 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/rmda_moe.h"
+
+#define RMDA_WAVE 64
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float rmda_h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint16_t rmda_f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Device-scope (L2-coherent) load, for data another workgroup of the same
+// grid wrote before a fence + atomic hand-off.
+__device__ __forceinline__ uint32_t rmda_load_agent(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Order-preserving map of a non-NaN float to uint32 (-0 and +0 map equal).
+__device__ __forceinline__ uint32_t rmda_float_key(float v) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if ((u & 0x7fffffffu) == 0) {
+        u = 0;
+    }
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float rmda_key_float(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __builtin_bit_cast(float, u);
+}
+
+// ---- launch helpers implemented by the kernel files ----
+// Every launcher validates nothing: api.hip checks shapes first.  They return
+// hipGetLastError() after the launch.
+
+// router.hip
+hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, const float *bias,
+                              float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
+                              uint32_t nbias, uint32_t *zero_words, uint32_t n_zero);
+
+// route.hip: top-k per row; count gets atomic adds (caller zeroes it first).
+hipError_t rmda_launch_route(hipStream_t s, const float *proj, uint32_t *idx, float *wt,
+                             uint32_t *count, uint32_t rows, uint32_t experts, uint32_t topk,
+                             uint32_t stride);
+
+// scan.hip
+hipError_t rmda_launch_zero(hipStream_t s, uint32_t *p, size_t n, uint32_t value);
+hipError_t rmda_launch_scan(hipStream_t s, const uint32_t *count, uint32_t *off, uint32_t *tiles,
+                            uint32_t n_tiles, uint32_t experts, uint32_t tile);
+
+// Ranking for the stable permutation.  Pairs are cut into blocks of
+// RMDA_RANK_BLOCK; lrank = rank of the pair among equal experts inside its
+// block, hist[b][e] = the block's per-expert count.  The last block to finish
+// turns hist into base offsets (boff[b][e] = off[e] + sum_{b'<b} hist[b'][e]),
+// writes off/count, and, when items != NULL, the grouped-GEMM work list.
+#define RMDA_RANK_BLOCK 1024u
+struct rmda_rank_args_t {
+    const uint32_t *idx;
+    uint32_t npairs;
+    uint32_t experts;
+    uint32_t tile;      // segment padding P for off
+    uint32_t *lrank;    // [npairs]
+    uint32_t *hist;     // [nblocks][experts], becomes boff in place
+    uint32_t *count;    // [experts] out, or NULL
+    uint32_t *off;      // [experts] out, or NULL
+    const uint32_t *off_in; // [experts] caller's offsets (then tile is unused), or NULL
+    uint32_t *done;     // one word, zero on entry, left zero
+    // work list (optional)
+    uint32_t *items;    // uint4 per item {expert, row0, rows, 0}
+    uint32_t *n_items;  // one word
+    uint32_t bm;        // rows per work item
+    uint32_t shared_rows; // rows of the shared-expert group (0 = none)
+    uint32_t shared_row0; // sorted-row base of the shared group
+};
+hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);
+
+// scatter.hip: slot[pr] = boff[pr/BLOCK][e] + lrank[pr]; optional row copy
+// (xp) and inverse map (rowtok[slot] = token).
+hipError_t rmda_launch_permute(hipStream_t s, const uint32_t *idx, const uint32_t *lrank,
+                               const uint32_t *boff, uint32_t npairs, uint32_t topk,
+                               uint32_t experts, uint32_t *slot, uint32_t *rowtok,
+                               const uint16_t *x16, uint16_t *xp, uint32_t d8);
+
+// gemm.hip: grouped GEMM over a device work list.
+enum {
+    RMDA_GEMM_SWIGLU = 0, // gate_up: A rows gathered via rowtok, out fp16 silu(g)*u
+    RMDA_GEMM_F16 = 1,    // down: A rows direct, out fp16
+    RMDA_GEMM_F32 = 2     // reference matmul_f16_moe: A rows direct, out fp32 * scale
+};
+struct rmda_gemm_args_t {
+    int mode;
+    const uint16_t *a;        // A base
+    const uint32_t *rowtok;   // SWIGLU: sorted row -> token
+    uint32_t lda;             // elements
+    const uint16_t *w;        // [groups][n_w][k]
+    const uint16_t *w_shared; // group == shared_group uses this [n_w][k]
+    uint32_t shared_group;    // RMDA_NONE if none
+    uint32_t shared_row0;     // SWIGLU: token = row - shared_row0 for the shared group
+    uint32_t n_w;             // rows of one group's weight matrix
+    uint32_t k;
+    uint32_t n_out;           // output columns (SWIGLU: inter; else n_w)
+    uint32_t inter;           // SWIGLU: up rows start at inter
+    void *out;
+    uint32_t ldo;             // elements
+    const uint32_t *items;    // uint4 {group, row0, rows, 0}
+    const uint32_t *n_items;  // device word, or NULL: use max_items
+    uint32_t max_items;       // grid bound
+    const uint32_t *tiles;    // F32 mode: reference tile map instead of items
+    const uint32_t *amax;
+    uint32_t sa, sb;
+};
+hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
+#define RMDA_GEMM_BM 128u
+
+// combine.hip
+hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, const float *wt,
+                               const uint32_t *slot, const float *y, const float *proj,
+                               const float *sh, const float *inj, float *h, uint16_t *out);
+// fused-layer combine: y fp16 rows, optional shared rows at shared_row0 + r.
+hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
+                                 const uint16_t *y, const float *proj, uint32_t pstride,
+                                 uint32_t sg_off, uint32_t shared_row0, int has_shared,
+                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk);
+
+// elem.hip
+hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y);
+hipError_t rmda_launch_absmax(hipStream_t s, const rmda_pc_absmax_t *pc, const float *x, uint32_t *amax);
+hipError_t rmda_launch_cast(hipStream_t s, const rmda_pc_cast_t *pc, const float *src, uint16_t *dst,
+                            const uint32_t *amax);
+hipError_t rmda_launch_bf16(hipStream_t s, uint32_t n, uint32_t *w);
+hipError_t rmda_launch_fill_normal(hipStream_t s, void *dst, size_t n, int f16, uint64_t stream,
+                                   uint64_t seed, float std);

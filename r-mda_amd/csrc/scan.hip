@@ -1,0 +1,277 @@
+// Expert offsets (moe_scan) and the deterministic ranking behind the stable
+// permutation (the order moe_scatter's atomics would give if the pairs ran
+// one after another).
+//
+// rank_kernel: pairs are cut into blocks of RMDA_RANK_BLOCK.  A 256-thread
+// workgroup walks its block 256 pairs at a time; each wave ORs a 64-bit lane
+// mask per expert in LDS, so a pair's rank among equal experts in its block
+// is (running count) + (masks of lower waves) + popcount(own mask & lanes
+// below).  The block's per-expert totals go to hist[b][e].  The last block to
+// finish (atomic ticket) converts hist into per-block base offsets, writes
+// off/count, and builds the grouped-GEMM work list, so the whole ranking is
+// one launch with no host round trip and no atomic-order dependence.
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t NT = 256;
+
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t *p, size_t n, uint32_t value) {
+    for (size_t i = blockIdx.x * (size_t)NT + threadIdx.x; i < n; i += (size_t)gridDim.x * NT) {
+        p[i] = value;
+    }
+}
+
+// Exclusive scan of one value per thread over a 256-thread block.
+__device__ uint32_t block_exscan(uint32_t v, uint32_t *sbuf, uint32_t *total) {
+    const uint32_t lane = threadIdx.x % RMDA_WAVE;
+    const uint32_t w = threadIdx.x / RMDA_WAVE;
+    uint32_t x = v;
+#pragma unroll
+    for (int o = 1; o < RMDA_WAVE; o <<= 1) {
+        uint32_t y = __shfl_up(x, o);
+        if (lane >= (uint32_t)o) {
+            x += y;
+        }
+    }
+    if (lane == RMDA_WAVE - 1) {
+        sbuf[w] = x;
+    }
+    __syncthreads();
+    uint32_t base = 0;
+    uint32_t tot = 0;
+    for (uint32_t i = 0; i < NT / RMDA_WAVE; i += 1) {
+        base += i < w ? sbuf[i] : 0u;
+        tot += sbuf[i];
+    }
+    __syncthreads();
+    *total = tot;
+    return base + x - v;
+}
+
+// shader/moe_scan.comp:14-37, one thread per expert (experts <= 512).
+// tiles[t] is written once per t: the owner is found by binary search over
+// the inclusive padded prefix instead of relying on a pre-fill.
+__global__ __launch_bounds__(512) void scan_kernel(const uint32_t *__restrict__ count,
+                                                   uint32_t *__restrict__ off,
+                                                   uint32_t *__restrict__ tiles,
+                                                   uint32_t n_tiles, uint32_t experts,
+                                                   uint32_t tile) {
+    __shared__ uint32_t s[512];
+    const uint32_t e = threadIdx.x;
+    uint32_t p = 0;
+    if (e < experts) {
+        p = (count[e] + tile - 1u) / tile * tile;
+    }
+    s[e] = p;
+    __syncthreads();
+    for (uint32_t dd = 1; dd < 512; dd <<= 1) {
+        uint32_t v = s[e];
+        if (e >= dd) {
+            v += s[e - dd];
+        }
+        __syncthreads();
+        s[e] = v;
+        __syncthreads();
+    }
+    if (e < experts) {
+        off[e] = s[e] - p;
+    }
+    for (uint32_t t = e; t < n_tiles; t += 512) {
+        // first expert whose inclusive end exceeds t*tile
+        const uint64_t row = (uint64_t)t * tile;
+        uint32_t lo = 0;
+        uint32_t hi = experts;
+        while (lo < hi) {
+            uint32_t mid = (lo + hi) / 2;
+            if ((uint64_t)s[mid] > row) {
+                hi = mid;
+            } else {
+                lo = mid + 1;
+            }
+        }
+        tiles[t] = lo < experts ? lo : RMDA_NONE;
+    }
+}
+
+__global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
+    __shared__ unsigned long long msk[NT / RMDA_WAVE][RMDA_MAX_EXPERTS];
+    __shared__ uint32_t run[RMDA_MAX_EXPERTS];
+    __shared__ uint32_t sbuf[NT / RMDA_WAVE];
+    __shared__ uint32_t s_last;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % RMDA_WAVE;
+    const uint32_t w = tid / RMDA_WAVE;
+    const uint32_t E = a.experts;
+    const uint32_t b = blockIdx.x;
+    const uint32_t nb = gridDim.x;
+
+    for (uint32_t e = tid; e < E; e += NT) {
+        run[e] = 0;
+    }
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (RMDA_WAVE - lane));
+    for (uint32_t it = 0; it < RMDA_RANK_BLOCK / NT; it += 1) {
+        for (uint32_t e = lane; e < E; e += RMDA_WAVE) {
+            msk[w][e] = 0ull;
+        }
+        __syncthreads();
+        const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
+        uint32_t e = RMDA_NONE;
+        if (pr < a.npairs) {
+            e = a.idx[pr];
+            if (e >= E) {
+                e = RMDA_NONE;
+            }
+        }
+        if (e != RMDA_NONE) {
+            atomicOr(&msk[w][e], 1ull << lane);
+        }
+        __syncthreads();
+        if (e != RMDA_NONE) {
+            uint32_t r = run[e];
+            for (uint32_t ww = 0; ww < w; ww += 1) {
+                r += __popcll(msk[ww][e]);
+            }
+            r += __popcll(msk[w][e] & below);
+            a.lrank[pr] = r;
+        }
+        __syncthreads();
+        for (uint32_t e2 = tid; e2 < E; e2 += NT) {
+            uint32_t add = 0;
+            for (uint32_t ww = 0; ww < NT / RMDA_WAVE; ww += 1) {
+                add += __popcll(msk[ww][e2]);
+            }
+            run[e2] += add;
+        }
+        __syncthreads();
+    }
+    for (uint32_t e = tid; e < E; e += NT) {
+        a.hist[(size_t)b * E + e] = run[e];
+    }
+
+    // hand-off: the last block to arrive finalises
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        // atomicInc wraps the ticket back to 0 on the last block
+        s_last = atomicInc(a.done, nb - 1) == nb - 1;
+    }
+    __syncthreads();
+    if (!s_last) {
+        return;
+    }
+    __threadfence();
+
+    // Each thread owns experts e0 = 2t and e0+1: column prefix of hist over
+    // blocks (other blocks' writes read at device scope), then padded widths,
+    // offsets, and per-block bases, all on entries this thread wrote itself.
+    const uint32_t e0 = 2 * tid;
+    uint32_t c0 = 0;
+    uint32_t c1 = 0;
+    for (uint32_t j = 0; j < 2; j += 1) {
+        const uint32_t e = e0 + j;
+        if (e < E) {
+            uint32_t acc = 0;
+            for (uint32_t bb = 0; bb < nb; bb += 1) {
+                uint32_t *hp = &a.hist[(size_t)bb * E + e];
+                const uint32_t h = rmda_load_agent(hp);
+                *hp = acc;
+                acc += h;
+            }
+            if (j == 0) {
+                c0 = acc;
+            } else {
+                c1 = acc;
+            }
+        }
+    }
+    const uint32_t p0 = (c0 + a.tile - 1u) / a.tile * a.tile;
+    const uint32_t p1 = (c1 + a.tile - 1u) / a.tile * a.tile;
+    uint32_t total = 0;
+    const uint32_t base = block_exscan(p0 + p1, sbuf, &total);
+    uint32_t o0 = base;
+    uint32_t o1 = base + p0;
+    if (a.off_in != nullptr) {
+        o0 = e0 < E ? a.off_in[e0] : 0u;
+        o1 = e0 + 1 < E ? a.off_in[e0 + 1] : 0u;
+    }
+    for (uint32_t j = 0; j < 2; j += 1) {
+        const uint32_t e = e0 + j;
+        if (e < E) {
+            const uint32_t o = j == 0 ? o0 : o1;
+            if (a.off != nullptr) {
+                a.off[e] = o;
+            }
+            if (a.count != nullptr) {
+                a.count[e] = j == 0 ? c0 : c1;
+            }
+            for (uint32_t bb = 0; bb < nb; bb += 1) {
+                a.hist[(size_t)bb * E + e] += o;
+            }
+        }
+    }
+    if (a.items == nullptr) {
+        return;
+    }
+    // grouped-GEMM work list: ceil(count/bm) items per expert, then the shared group
+    const uint32_t n0 = (c0 + a.bm - 1u) / a.bm;
+    const uint32_t n1 = (c1 + a.bm - 1u) / a.bm;
+    uint32_t routed = 0;
+    const uint32_t ib = block_exscan(n0 + n1, sbuf, &routed);
+    for (uint32_t j = 0; j < 2; j += 1) {
+        const uint32_t e = e0 + j;
+        const uint32_t c = j == 0 ? c0 : c1;
+        const uint32_t ni = j == 0 ? n0 : n1;
+        const uint32_t first = j == 0 ? ib : ib + n0;
+        const uint32_t o = j == 0 ? o0 : o1;
+        for (uint32_t i = 0; i < ni; i += 1) {
+            uint4 it;
+            it.x = e;
+            it.y = o + i * a.bm;
+            it.z = min(a.bm, c - i * a.bm);
+            it.w = 0;
+            reinterpret_cast<uint4 *>(a.items)[first + i] = it;
+        }
+    }
+    const uint32_t ns = (a.shared_rows + a.bm - 1u) / a.bm;
+    for (uint32_t i = tid; i < ns; i += NT) {
+        uint4 it;
+        it.x = E;
+        it.y = a.shared_row0 + i * a.bm;
+        it.z = min(a.bm, a.shared_rows - i * a.bm);
+        it.w = 0;
+        reinterpret_cast<uint4 *>(a.items)[routed + i] = it;
+    }
+    if (tid == 0) {
+        *a.n_items = routed + ns;
+    }
+}
+
+}  // namespace
+
+hipError_t rmda_launch_zero(hipStream_t s, uint32_t *p, size_t n, uint32_t value) {
+    if (n == 0) {
+        return hipSuccess;
+    }
+    size_t blocks = (n + NT - 1) / NT;
+    if (blocks > 1024) {
+        blocks = 1024;
+    }
+    hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)blocks), dim3(NT), 0, s, p, n, value);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_scan(hipStream_t s, const uint32_t *count, uint32_t *off, uint32_t *tiles,
+                            uint32_t n_tiles, uint32_t experts, uint32_t tile) {
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(512), 0, s, count, off, tiles, n_tiles, experts, tile);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
+    uint32_t nb = (a->npairs + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
+    if (nb == 0) {
+        nb = 1;  // one block still finalises (zero counts, empty work list)
+    }
+    hipLaunchKernelGGL(rank_kernel, dim3(nb), dim3(NT), 0, s, *a);
+    return hipGetLastError();
+}

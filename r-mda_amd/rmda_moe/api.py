@@ -1,0 +1,206 @@
+"""Python mirror of the C ABI (include/rmda_moe.h) over torch device tensors.
+
+Method names and argument order follow the reference's per-kernel recording
+calls (mda_vkc_run with the push-constant struct and buffers in binding
+order, src/qwen.c:770-907); torch only supplies device memory and the stream.
+Every call goes through librmda_moe.so and raises MoeError on a non-zero
+status, carrying the context's sticky message.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import (NONE, NO_SLOT, Bf16PC, CombinePC, ElemPC, LayerArgs, MmPC, RoutePC, RouterPC,
+                   ScanPC, ScatterPC, Shape, SlotPC, WsLayout)
+
+
+class MoeError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__("%s (%d): %s" % (_lib.ERRORS.get(code, "?"), code, message))
+        self.code = code
+        self.message = message
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def _u32(t):
+    """Reinterpret an int32 tensor as the uint32 buffers of the ABI (no copy)."""
+    return t
+
+
+def shape_struct(shape):
+    return Shape(shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"], shape["shared"])
+
+
+def workspace_bytes(shape):
+    """rmda_moe_workspace_bytes; 0 means the shape is rejected.  Host-only."""
+    s = shape_struct(shape)
+    return _lib.lib().rmda_moe_workspace_bytes(ctypes.byref(s))
+
+
+def workspace_layout(shape):
+    s = shape_struct(shape)
+    lay = WsLayout()
+    rc = _lib.lib().rmda_moe_workspace_layout(ctypes.byref(s), ctypes.byref(lay))
+    if rc != 0:
+        raise MoeError(rc, "workspace layout rejected the shape")
+    return {k: getattr(lay, k) for k, _ in WsLayout._fields_}
+
+
+class Context:
+    """One rmda_moe_ctx_t bound to a device and a stream (torch's current one
+    by default)."""
+
+    def __init__(self, device=0, stream=None):
+        self.L = _lib.lib()
+        self.device = device
+        h = ctypes.c_void_p()
+        raw = self._raw_stream(stream)
+        rc = self.L.rmda_moe_ctx_create(ctypes.byref(h), device, raw)
+        if rc != 0:
+            raise MoeError(rc, "rmda_moe_ctx_create failed")
+        self.h = h
+
+    @staticmethod
+    def _raw_stream(stream):
+        if stream is None:
+            return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if isinstance(stream, int):
+            return ctypes.c_void_p(stream)
+        return ctypes.c_void_p(stream.cuda_stream)
+
+    def close(self):
+        if getattr(self, "h", None) is not None:
+            self.L.rmda_moe_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream):
+        self._check(self.L.rmda_moe_set_stream(self.h, self._raw_stream(stream)))
+
+    def _check(self, rc):
+        if rc != 0:
+            msg = self.L.rmda_moe_ctx_message(self.h)
+            raise MoeError(rc, msg.decode() if msg else "")
+
+    def error(self):
+        return self.L.rmda_moe_ctx_error(self.h)
+
+    def message(self):
+        msg = self.L.rmda_moe_ctx_message(self.h)
+        return msg.decode() if msg else ""
+
+    def clear_error(self):
+        self.L.rmda_moe_ctx_clear_error(self.h)
+
+    def sync(self):
+        self._check(self.L.rmda_moe_sync(self.h))
+
+    # ---- per-stage drop-ins ----
+
+    def route(self, rows, experts, topk, stride, proj, idx, wt, count):
+        pc = RoutePC(rows, experts, topk, stride)
+        self._check(self.L.rmda_moe_route(self.h, ctypes.byref(pc), _ptr(proj), _ptr(idx), _ptr(wt),
+                                          _ptr(count)))
+
+    def scan(self, experts, tile, count, off, tiles, n_tiles):
+        pc = ScanPC(experts, tile)
+        self._check(self.L.rmda_moe_scan(self.h, ctypes.byref(pc), _ptr(count), _ptr(off), _ptr(tiles),
+                                         n_tiles))
+
+    def scatter_experts(self, experts):
+        self._check(self.L.rmda_moe_scatter_experts(self.h, experts))
+
+    def scatter(self, rows, topk, d8, idx, off, fill, x16, xp, slot):
+        pc = ScatterPC(rows, topk, d8)
+        self._check(self.L.rmda_moe_scatter(self.h, ctypes.byref(pc), _ptr(idx), _ptr(off), _ptr(fill),
+                                            _ptr(x16), _ptr(xp), _ptr(slot)))
+
+    def mm(self, m, n, k, sa, sb, a, b, c, amax, tiles):
+        pc = MmPC(m, n, k, sa, sb)
+        self._check(self.L.rmda_moe_mm(self.h, ctypes.byref(pc), _ptr(a), _ptr(b), _ptr(c), _ptr(amax),
+                                       _ptr(tiles)))
+
+    def combine(self, pc_fields, wt, slot, y, proj, sh, inj, h):
+        pc = CombinePC(*pc_fields)
+        self._check(self.L.rmda_moe_combine(self.h, ctypes.byref(pc), _ptr(wt), _ptr(slot), _ptr(y),
+                                            _ptr(proj), _ptr(sh), _ptr(inj), _ptr(h)))
+
+    def combine_plain(self, pc_fields, wt, slot, y, proj, sh, out):
+        pc = CombinePC(*pc_fields)
+        self._check(self.L.rmda_moe_combine_plain(self.h, ctypes.byref(pc), _ptr(wt), _ptr(slot), _ptr(y),
+                                                  _ptr(proj), _ptr(sh), _ptr(out)))
+
+    def qwen_elem(self, rows, n, astride, ao, bo, op, scale, a, y):
+        pc = ElemPC(rows, n, astride, ao, bo, op, scale)
+        self._check(self.L.rmda_qwen_elem(self.h, ctypes.byref(pc), _ptr(a), _ptr(y)))
+
+    def absmax(self, n, slot, x, amax):
+        pc = SlotPC(n, slot)
+        self._check(self.L.rmda_absmax(self.h, ctypes.byref(pc), _ptr(x), _ptr(amax)))
+
+    def cast_f16(self, n, slot, src, dst, amax):
+        pc = SlotPC(n, slot)
+        self._check(self.L.rmda_cast_f16(self.h, ctypes.byref(pc), _ptr(src), _ptr(dst), _ptr(amax)))
+
+    def qwen_bf16(self, n, w):
+        pc = Bf16PC(n)
+        self._check(self.L.rmda_qwen_bf16(self.h, ctypes.byref(pc), _ptr(w)))
+
+    def router(self, rows, d, cols, stride, nbias, x16, w, bias, proj):
+        pc = RouterPC(rows, d, cols, stride, nbias)
+        self._check(self.L.rmda_moe_router(self.h, ctypes.byref(pc), _ptr(x16), _ptr(w), _ptr(bias),
+                                           _ptr(proj)))
+
+    # ---- fused layer ----
+
+    def layer(self, shape, x, w_router, bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down, out, workspace):
+        s = shape_struct(shape)
+        args = LayerArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(w_gate_up), _ptr(w_down),
+                         _ptr(w_sh_gate_up), _ptr(w_sh_down), _ptr(out), _ptr(workspace),
+                         workspace.numel() * workspace.element_size())
+        self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
+
+    def fill_normal(self, t, stream, seed, std):
+        if t.dtype == torch.float16:
+            self._check(self.L.rmda_moe_fill_normal_f16(self.h, _ptr(t), t.numel(), stream, seed, std))
+        elif t.dtype == torch.float32:
+            self._check(self.L.rmda_moe_fill_normal_f32(self.h, _ptr(t), t.numel(), stream, seed, std))
+        else:
+            raise ValueError("fill_normal supports float16 and float32")
+
+
+def ws_views(shape, workspace):
+    """Typed views of the routing intermediates inside a layer workspace."""
+    lay = workspace_layout(shape)
+    T, K, E = shape["rows"], shape["topk"], shape["experts"]
+    base = workspace
+
+    def view(off, n, dtype):
+        nbytes = n * torch.tensor([], dtype=dtype).element_size()
+        return base[off:off + nbytes].view(dtype)
+
+    return {
+        "proj": view(lay["proj"], T * lay["proj_stride"], torch.float32).view(T, lay["proj_stride"]),
+        "idx": view(lay["idx"], T * K, torch.int32),
+        "wt": view(lay["wt"], T * K, torch.float32),
+        "count": view(lay["count"], E, torch.int32),
+        "off": view(lay["off"], E, torch.int32),
+        "slot": view(lay["slot"], T * K, torch.int32),
+    }

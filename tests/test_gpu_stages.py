@@ -1,0 +1,320 @@
+"""Per-stage parity of the HIP drop-ins against the CPU oracle, through the C ABI.
+
+Integer/index outputs (idx, count, off, tiles, slot, fill, permuted rows,
+router logits) must be bit-exact; floating-point outputs are held to the
+tolerances written in each test.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import dev, empty_u32, f32, u16, u32
+from oracle import oracle as orc
+from rmda_moe import api, configs
+
+pytestmark = pytest.mark.gpu
+
+NONE = 0xFFFFFFFF
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    torch.cuda.set_device(0)
+    c = api.Context(0)
+    yield c
+    c.close()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- generator
+
+@pytest.mark.parametrize("n,stream,seed,std", [(100003, 3, 0, 0.02), (4096, 1, 7, 1.0)])
+def test_fill_matches_oracle_bitwise(ctx, n, stream, seed, std):
+    t16 = torch.empty(n, dtype=torch.float16, device="cuda")
+    t32 = torch.empty(n, dtype=torch.float32, device="cuda")
+    ctx.fill_normal(t16, stream, seed, std)
+    ctx.fill_normal(t32, stream, seed, std)
+    ctx.sync()
+    assert np.array_equal(u16(t16), orc.fill_normal_f16(n, stream, seed, std))
+    assert np.array_equal(t32.cpu().numpy().view(np.uint32), orc.fill_normal_f32(n, stream, seed, std).view(np.uint32))
+
+
+# ---------------------------------------------------------------- router (A0)
+
+@pytest.mark.parametrize("rows,d,cols,stride,bias", [
+    (256, 512, 8, 8, False),       # config 1
+    (2048, 2048, 128, 128, False),  # config 3
+    (2048, 2048, 128, 130, True),   # config 4 (skew bias), padded stride
+    (512, 2048, 513, 513, False),   # config 5 row subset: 512 experts + shared gate
+    (37, 256, 70, 72, True),        # ragged tile edges
+])
+def test_router_bitexact(ctx, rows, d, cols, stride, bias):
+    x = orc.fill_normal_f16(rows * d, configs.STREAM_X, 1, 1.0).reshape(rows, d)
+    w = orc.fill_normal_f32(cols * d, configs.STREAM_W_ROUTER, 1, 0.02).reshape(cols, d)
+    b = configs.skew_bias(cols, 1) if bias else None
+    nbias = cols if bias else 0
+    ref = orc.router(x, w, b, nbias=nbias, stride=stride)
+    proj = torch.full((rows, stride), 7.0, dtype=torch.float32, device="cuda")
+    ctx.router(rows, d, cols, stride, nbias, dev(x), dev(w), None if b is None else dev(b), proj)
+    ctx.sync()
+    got = proj.cpu().numpy()
+    assert np.array_equal(got[:, :cols].view(np.uint32), ref[:, :cols].view(np.uint32))
+    assert np.all(got[:, cols:] == 7.0), "columns beyond cols must stay untouched"
+
+
+# ---------------------------------------------------------------- route (A1)
+
+def planted_logits(rows, experts, stride, seed):
+    r = rng(seed)
+    p = r.standard_normal((rows, stride)).astype(np.float32)
+    p[:, experts:] = 1e30  # padding columns must never be read
+    # exact ties: copy a value to several columns
+    for i in range(0, rows, 7):
+        cols = r.choice(experts, size=min(4, experts), replace=False)
+        p[i, cols] = p[i, cols[0]]
+    # NaN / -inf / <= -3e38 are never selectable
+    for i in range(3, rows, 11):
+        p[i, r.integers(experts)] = np.nan
+        p[i, r.integers(experts)] = -np.inf
+        p[i, r.integers(experts)] = -3.0e38
+        p[i, r.integers(experts)] = -3.3e38
+    # +0 / -0 tie
+    if rows > 5 and experts > 3:
+        p[5, :experts] = -1.0
+        p[5, 1] = -0.0
+        p[5, 3] = 0.0
+    # whole row of equal values: order must be 0, 1, 2, ...
+    p[0, :experts] = 0.25
+    return p
+
+
+@pytest.mark.parametrize("rows,experts,topk,stride", [
+    (256, 8, 2, 8), (333, 128, 8, 160), (64, 512, 10, 513), (50, 512, 16, 512),
+    (40, 16, 16, 16), (77, 100, 1, 100), (9, 64, 3, 64),
+])
+def test_route_bitexact(ctx, rows, experts, topk, stride):
+    p = planted_logits(rows, experts, stride, seed=rows + experts)
+    idx_r, wt_r, cnt_r = orc.route(p, experts, topk)
+    idx = empty_u32(rows * topk)
+    wt = torch.empty(rows * topk, dtype=torch.float32, device="cuda")
+    cnt = empty_u32(experts, fill=12345)  # must be overwritten, not added to
+    ctx.route(rows, experts, topk, stride, dev(p), idx, wt, cnt)
+    ctx.sync()
+    assert np.array_equal(u32(idx), idx_r)
+    assert np.array_equal(u32(cnt), cnt_r)
+    np.testing.assert_allclose(wt.cpu().numpy(), wt_r, rtol=2e-6, atol=1e-7)
+
+
+def test_route_unselectable_rows(ctx):
+    # fewer selectable columns than topk: the remaining picks are RMDA_NONE
+    rows, experts, topk = 4, 8, 4
+    p = np.full((rows, experts), np.nan, np.float32)
+    p[0, 2] = 1.0
+    p[1, :] = -np.inf
+    p[2, 5] = 3.0
+    p[2, 6] = 3.0
+    p[3, :] = -3.0e38
+    idx_r, wt_r, cnt_r = orc.route(p, experts, topk)
+    idx = empty_u32(rows * topk)
+    wt = torch.empty(rows * topk, dtype=torch.float32, device="cuda")
+    cnt = empty_u32(experts)
+    ctx.route(rows, experts, topk, experts, dev(p), idx, wt, cnt)
+    ctx.sync()
+    assert np.array_equal(u32(idx), idx_r)
+    assert np.array_equal(u32(cnt), cnt_r)
+    assert u32(idx)[0] == 2 and u32(idx)[1] == NONE
+    np.testing.assert_allclose(wt.cpu().numpy(), wt_r, rtol=2e-6, atol=1e-7, equal_nan=True)
+
+
+# ---------------------------------------------------------------- scan (A2)
+
+@pytest.mark.parametrize("experts,tile", [(8, 128), (128, 128), (128, 1), (512, 128), (512, 16), (300, 7)])
+def test_scan_bitexact(ctx, experts, tile):
+    r = rng(experts * 31 + tile)
+    cnt = r.integers(0, 400, experts).astype(np.uint32)
+    cnt[r.choice(experts, experts // 5, replace=False)] = 0  # empty experts
+    n_tiles = int((cnt.sum() + experts * (tile - 1)) // tile + 3)
+    off_r, tiles_r = orc.scan(cnt, tile, n_tiles)
+    off = empty_u32(experts)
+    tiles = empty_u32(n_tiles, fill=0x5A5A5A5A)
+    ctx.scan(experts, tile, dev(cnt), off, tiles, n_tiles)
+    ctx.sync()
+    assert np.array_equal(u32(off), off_r)
+    assert np.array_equal(u32(tiles), tiles_r)
+
+
+# ---------------------------------------------------------------- scatter (A3)
+
+@pytest.mark.parametrize("rows,experts,topk,d,mode", [
+    (2048, 128, 8, 2048, "route"),   # config-3 sized
+    (256, 8, 2, 512, "route"),       # config 1
+    (1000, 64, 4, 256, "random"),    # arbitrary idx with repeats and NONE
+    (4096, 512, 10, 128, "route"),   # several rank blocks, 512 experts
+])
+def test_scatter_bitexact(ctx, rows, experts, topk, d, mode):
+    r = rng(rows + d)
+    if mode == "route":
+        p = r.standard_normal((rows, experts)).astype(np.float32)
+        idx_r, _, cnt_r = orc.route(p, experts, topk)
+    else:
+        idx_r = r.integers(0, experts, rows * topk).astype(np.uint32)
+        idx_r[r.choice(rows * topk, rows // 3, replace=False)] = NONE
+        cnt_r = np.bincount(idx_r[idx_r != NONE], minlength=experts).astype(np.uint32)
+    tile = 128
+    mrows = int(((rows * topk + experts * (tile - 1)) + tile - 1) // tile * tile)
+    off_r, _ = orc.scan(cnt_r, tile, mrows // tile)
+    x = orc.fill_normal_f16(rows * d, 1, 5, 1.0).reshape(rows, d)
+    xp_r, slot_r, fill_r = orc.scatter(idx_r, off_r, x, topk, mrows)
+    ctx.scatter_experts(experts)
+    fill = empty_u32(experts, fill=777)
+    slot = empty_u32(rows * topk)
+    xp = torch.zeros(mrows, d, dtype=torch.float16, device="cuda")
+    ctx.scatter(rows, topk, d // 8, dev(idx_r), dev(off_r), fill, dev(x), xp, slot)
+    ctx.sync()
+    assert np.array_equal(u32(slot), slot_r)
+    assert np.array_equal(u32(fill), fill_r)
+    assert np.array_equal(u16(xp), xp_r)
+    # the permutation is the stable counting sort of idx
+    valid = idx_r != NONE
+    order = np.argsort(idx_r[valid], kind="stable")
+    pos = np.empty(order.size, np.int64)
+    pos[order] = np.arange(order.size)
+    e = idx_r[valid].astype(np.int64)
+    start = np.concatenate([[0], np.cumsum(cnt_r)])[:-1]
+    assert np.array_equal(u32(slot)[valid] - off_r[e], pos - start[e])
+
+
+def test_scatter_twice_deterministic(ctx):
+    rows, experts, topk, d = 3000, 128, 8, 64
+    p = rng(3).standard_normal((rows, experts)).astype(np.float32)
+    idx_r, _, cnt_r = orc.route(p, experts, topk)
+    off_r, _ = orc.scan(cnt_r, 1, 0)
+    ctx.scatter_experts(experts)
+    outs = []
+    for _ in range(2):
+        slot = empty_u32(rows * topk)
+        fill = empty_u32(experts)
+        xp = torch.zeros(rows * topk, d, dtype=torch.float16, device="cuda")
+        x = torch.randn(rows, d, device="cuda", generator=torch.Generator("cuda").manual_seed(1)).half()
+        ctx.scatter(rows, topk, d // 8, dev(idx_r), dev(off_r), fill, x, xp, slot)
+        ctx.sync()
+        outs.append((u32(slot), u16(xp)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+# ---------------------------------------------------------------- grouped GEMM (A4/A7, drop-in)
+
+@pytest.mark.parametrize("m,n,k,E,scaled", [(512, 256, 512, 3, False), (640, 1536, 2048, 5, True),
+                                           (256, 128, 32, 2, False)])
+def test_moe_mm_vs_oracle(ctx, m, n, k, E, scaled):
+    r = rng(m + n + k)
+    ntile = m // 128
+    tiles = r.integers(0, E, ntile).astype(np.uint32)
+    tiles[r.choice(ntile, max(1, ntile // 4), replace=False)] = NONE
+    a = orc.fill_normal_f16(m * k, 11, m, 1.0).reshape(m, k)
+    b = orc.fill_normal_f16(E * n * k, 12, n, 0.02).reshape(E, n, k)
+    amax = np.zeros(4, np.uint32)
+    sa = sb = 0xFFFFFFFF
+    if scaled:
+        amax[1] = np.float32(3.7).view(np.uint32)
+        amax[2] = np.float32(0.0).view(np.uint32)  # zero amax -> scale 1
+        sa, sb = 1, 2
+    ref = orc.moe_mm(a, b, tiles, n, k, sa=sa, sb=sb, amax=amax, c_init=np.full((m, n), 1e30, np.float32))
+    c = torch.full((m, n), 1e30, dtype=torch.float32, device="cuda")
+    ctx.mm(m, n, k, sa, sb, dev(a), dev(b), c, dev(amax), dev(tiles))
+    ctx.sync()
+    got = c.cpu().numpy()
+    skip = np.repeat(tiles == NONE, 128)
+    assert np.all(got[skip] == 1e30), "rows of unused tiles must stay untouched"
+    live = ~skip
+    err = np.abs(got[live] - ref[live]).max()
+    assert err <= 1e-5 * max(1.0, np.abs(ref[live]).max()), err
+
+
+# ---------------------------------------------------------------- combine (A9) and helpers
+
+@pytest.mark.parametrize("shared,hc", [(False, 4), (True, 4), (True, 0)])
+def test_combine_vs_oracle(ctx, shared, hc):
+    r = rng(17)
+    rows, d, topk, E = 300, 256, 8, 64
+    nrows = rows * topk + 50
+    p = r.standard_normal((rows, E + 3)).astype(np.float32)
+    idx, wt, cnt = orc.route(p, E, topk)
+    slot = r.permutation(nrows)[: rows * topk].astype(np.uint32)
+    slot[5] = NONE
+    y = r.standard_normal((nrows, d)).astype(np.float32)
+    sh = r.standard_normal((rows, d)).astype(np.float32) if shared else None
+    inj = r.standard_normal((rows, 10)).astype(np.float32)
+    fields = (rows, d, topk, E + 3, E, 10, 3, hc)
+    if hc:
+        h0 = r.standard_normal((rows, hc, d)).astype(np.float32)
+        ref = orc.combine(fields, wt, slot, y, p, sh, inj, h0)
+        h = dev(h0)
+        ctx.combine(fields, dev(wt), dev(slot), dev(y), dev(p), None if sh is None else dev(sh), dev(inj), h)
+        ctx.sync()
+        np.testing.assert_allclose(h.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    else:
+        ref = orc.combine_plain(fields, wt, slot, y, p, sh)
+        out = torch.empty(rows, d, dtype=torch.float16, device="cuda")
+        ctx.combine_plain(fields, dev(wt), dev(slot), dev(y), dev(p), None if sh is None else dev(sh), out)
+        ctx.sync()
+        np.testing.assert_allclose(f32(out), orc.h2f(orc.f2h(ref)), rtol=0, atol=2e-3)
+
+
+def test_elem_absmax_cast_bf16(ctx):
+    r = rng(23)
+    rows, n = 97, 640
+    a = (r.standard_normal((rows, 2 * n + 5)) * 3).astype(np.float32)
+    for op, scale in [(0, 1.0), (1, 0.5)]:
+        ref = orc.qwen_elem(a, rows, n, 2 * n + 5, 2, n + 3, op, scale)
+        y = torch.empty(rows * n, dtype=torch.float32, device="cuda")
+        ctx.qwen_elem(rows, n, 2 * n + 5, 2, n + 3, op, scale, dev(a), y)
+        ctx.sync()
+        np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+    x = (r.standard_normal(100000) * 5).astype(np.float32)
+    amax0 = np.array([0, np.float32(1.0).view(np.uint32), 0], np.uint32)
+    ref_amax = orc.absmax(x, amax0, 2)
+    amax = dev(amax0)
+    ctx.absmax(x.size, 2, dev(x), amax)
+    ctx.sync()
+    assert np.array_equal(u32(amax), ref_amax)
+    for slot in [2, 0xFFFFFFFF]:
+        ref16 = orc.cast_f16(x, ref_amax, slot)
+        dst = torch.empty(x.size, dtype=torch.float16, device="cuda")
+        ctx.cast_f16(x.size, slot, dev(x), dst, dev(ref_amax))
+        ctx.sync()
+        assert np.array_equal(u16(dst), ref16)
+    w = r.integers(0, 2 ** 32, 5000, dtype=np.uint64).astype(np.uint32)
+    w &= ~np.uint32(0x7F807F80)  # keep exponents small enough for fp16 range tests...
+    w |= np.uint32(0x3C003C00)   # ...and in the normal fp16 range
+    refw = orc.qwen_bf16(w)
+    wd = dev(w)
+    ctx.qwen_bf16(w.size, wd)
+    ctx.sync()
+    assert np.array_equal(u32(wd), refw)
+
+
+# ---------------------------------------------------------------- error behaviour
+
+def test_errors_are_sticky_and_reported(ctx):
+    c = api.Context(0)
+    idx = empty_u32(8)
+    wt = torch.empty(8, dtype=torch.float32, device="cuda")
+    cnt = empty_u32(600)
+    p = torch.zeros(4, 600, device="cuda")
+    with pytest.raises(api.MoeError) as e:
+        c.route(4, 600, 2, 600, p, idx, wt, cnt)  # experts > 512
+    assert e.value.code == -2
+    with pytest.raises(api.MoeError) as e:
+        c.route(4, 8, 2, 8, p, idx, wt, cnt)  # valid call after a failure: sticky
+    assert e.value.code == -5
+    c.clear_error()
+    c.route(4, 8, 2, 600, p, idx, wt, cnt)
+    c.sync()
+    with pytest.raises(api.MoeError) as e:
+        c.mm(100, 128, 32, 0xFFFFFFFF, 0xFFFFFFFF, p, p, p, None, idx)  # m % 128 != 0
+    assert e.value.code == -2
+    c.close()
