@@ -1,0 +1,259 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X (gfx950).
+
+One step = one call of rmda_moe_layer (router -> top-k -> ranks/offsets ->
+permutation -> grouped SwiGLU gate_up GEMM -> grouped down GEMM -> combine)
+over one batch of synthetic tokens already resident in HBM.  The default
+workload is BASELINE configuration 3 (T=2048, d=2048, 128 experts, top-8,
+I=768), the configuration the headline metric is quoted on.
+
+Prints ONE JSON line.  Besides the driver's fields it carries
+  roofline      the dominant kernel's algorithmic bytes (or FLOPs) per launch
+                divided by its average duration, measured with hipEvents on
+                the stream the kernels run on (the library's stage profiler);
+  stages        every stage's average duration and achieved rate;
+  gemm          grouped-GEMM FLOP rate against the dense fp16 MFMA peak and
+                against the weight-streaming ceiling min(peak, BW * AI);
+  cpu_baseline  the CPU oracle (a C restatement of the reference shaders)
+                timed on this host on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "r-mda_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE-layer tokens/sec at T=2048; grouped-GEMM % fp16 MFMA peak; HBM GB/s"
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gate_up_prefill_traffic.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3, help="BASELINE configuration (1-5)")
+    ap.add_argument("--cpu-tokens", type=int, default=None,
+                    help="tokens in the CPU-baseline sample (default: sized for ~10-30 s)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a device copy of known size (HBM counter calibration)")
+    ap.add_argument("--stages", action="store_true", help="print the stage table to stderr")
+    return ap.parse_args()
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def read_traffic():
+    """HBM bytes per gate_up launch from the committed PMC summary, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(TRAFFIC_FILE).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(inp, cfg, n_tokens):
+    """Time the CPU oracle's layer on a sample of tokens (routing covers all
+    tokens, the expert FFNs only the sample); tokens/s over the sample."""
+    import numpy as np
+    from oracle import oracle as orc
+    from rmda_moe import inputs
+
+    host = inputs.to_host(inp)
+    T = cfg["rows"]
+    n = min(n_tokens, T)
+    sel = np.arange(0, T, max(1, T // n), dtype=np.uint32)[:n]
+    th = cpu_threads()
+    orc.lib()
+    t0 = time.perf_counter()
+    orc.layer(host, tile=1, rows_sel=sel, threads=th)
+    dt = time.perf_counter() - t0
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(len(sel) / dt, 2),
+        "unit": "tokens/s",
+        "cores": th,
+        "kind": "port",
+        "sample": "%d of %d tokens (every %d-th) through the CPU oracle's full layer "
+                  "(router+top-k for all %d tokens, expert FFNs for the sample), %d threads, %.1f s, %s"
+                  % (len(sel), T, max(1, T // n), T, th, dt, model),
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the MoE layer on a single MI355X "
+              "(expert-parallel sharding is a design note, not built); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from rmda_moe import api, configs, inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    cfg = configs.CONFIGS[args.config]
+    ctx = api.Context(0)
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    shape = inp["shape"]
+    ws = inputs.workspace_for(shape)
+    out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
+
+    def step():
+        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
+                  inp["w_sh_gate_up"], inp["w_sh_down"], out, ws)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    torch.cuda.synchronize()
+
+    # timed region: K layer calls, bracketed by device synchronisation
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = ev0.elapsed_time(ev1) / args.steps
+
+    # per-stage durations: the same K calls again with the stage profiler on
+    ctx.prof_begin()
+    for _ in range(args.steps):
+        step()
+    stage_ms, n_prof = ctx.prof_end()
+    stage_us = {k: 1000.0 * v / max(n_prof, 1) for k, v in stage_ms.items()}
+
+    views = api.ws_views(shape, ws)
+    counts = views["count"].cpu().numpy()
+    touched = int((counts > 0).sum())
+    work = configs.algorithmic_work(cfg, touched=touched)
+
+    rate = {
+        "router": (work["router_bytes"], work["router_flops"]),
+        "route": (work["route_bytes"], 0),
+        "rank": (0, 0),
+        "permute": (0, 0),
+        "gate_up": (work["gate_up_bytes"], work["gate_up_flops"]),
+        "down": (work["down_bytes"], work["down_flops"]),
+        "combine": (work["combine_bytes"], 0),
+    }
+    stages = {}
+    for k, us in stage_us.items():
+        b, f = rate[k]
+        stages[k] = {"us": round(us, 2)}
+        if b:
+            stages[k]["GB/s"] = round(b / (us * 1e-6) / 1e9, 1)
+        if f:
+            stages[k]["TFLOP/s"] = round(f / (us * 1e-6) / 1e12, 1)
+
+    dom = max(stage_us, key=stage_us.get)
+    b, f = rate[dom]
+    ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    t_dom = stage_us[dom] * 1e-6
+    if f and b and f / b > ridge:
+        roof = {"bound": "mfma", "achieved": round(f / t_dom / 1e12, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(b / t_dom / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["kernel"] = dom
+    roof["algorithmic_bytes"] = b
+    roof["algorithmic_flops"] = f
+    roof["avg_us"] = round(stage_us[dom], 2)
+    roof["traffic"] = read_traffic() if (dom == "gate_up" and args.config == 3) else None
+
+    gemm_us = stage_us["gate_up"] + stage_us["down"]
+    gemm_tf = work["gemm_flops"] / (gemm_us * 1e-6) / 1e12
+    ai = work["gemm_flops"] / (work["gate_up_bytes"] + work["down_bytes"])
+    ceiling = min(PEAK_FP16_TFLOPS, PEAK_HBM_GBS * 1e9 * ai / 1e12)
+    gemm = {"TFLOP/s": round(gemm_tf, 1), "frac_of_fp16_peak": round(gemm_tf / PEAK_FP16_TFLOPS, 4),
+            "ai_flop_per_byte": round(ai, 1), "ceiling_TFLOP/s": round(ceiling, 1),
+            "frac_of_ceiling": round(gemm_tf / ceiling, 4), "experts_touched": touched}
+    hbm_small = {"combine_GB/s": stages["combine"].get("GB/s")}
+
+    if args.calib_copy:
+        # a plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("calib copy: %d bytes read, %d bytes written per launch" % (n, n), file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        n_tok = args.cpu_tokens
+        if n_tok is None:
+            n_tok = {1: 256, 2: 128, 3: 1024, 4: 1024, 5: 512}[args.config]
+        cpu = cpu_baseline(inp, cfg, n_tok)
+
+    if args.stages:
+        for k, v in stages.items():
+            print("%-8s %s" % (k, v), file=sys.stderr)
+
+    T = shape["rows"]
+    line = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (counter-hash N(0,1) activations, N(0,0.02) weights, seed 0)",
+        "config": {"workload": "%s: T=%d d=%d experts=%d top-%d inter=%d shared=%d%s (BASELINE config %d)"
+                               % (cfg["name"], T, shape["d"], shape["experts"], shape["topk"], shape["inter"],
+                                  shape["shared"], " skewed" if cfg.get("skew") else "", args.config),
+                   "tokens": T, "d": shape["d"], "experts": shape["experts"], "topk": shape["topk"],
+                   "inter": shape["inter"], "shared": shape["shared"], "parallelism": "single GPU"},
+        "wall_ms_per_step": round(1000.0 * wall / args.steps, 5),
+        "roofline": roof,
+        "gemm": gemm,
+        "hbm": hbm_small,
+        "stages": stages,
+        "cpu_baseline": cpu,
+    }
+    if cpu is not None:
+        line["cpu_baseline"]["gpu_over_cpu"] = round(line["value"] / cpu["value"], 1)
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

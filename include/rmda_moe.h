@@ -311,6 +311,35 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
                    const rmda_moe_layer_args_t *args);
 
+/* ---- stage profiler (replaces the reference's timestamp profiler:
+ * mda_vkc_prof_begin / mda_vkc_prof_mark / mda_vkc_prof_report,
+ * src/vkc.c:580-653, which writes a timestamp after every dispatch) ---- */
+
+/* Stages of rmda_moe_layer, in launch order. */
+enum {
+    RMDA_STAGE_ROUTER = 0,  /* router projection (fp32 logits)           */
+    RMDA_STAGE_ROUTE = 1,   /* top-k gating                              */
+    RMDA_STAGE_RANK = 2,    /* counts, offsets, stable ranks, work list  */
+    RMDA_STAGE_PERMUTE = 3, /* slots + sorted-row -> token map           */
+    RMDA_STAGE_GATE_UP = 4, /* grouped gate_up GEMM with SwiGLU epilogue */
+    RMDA_STAGE_DOWN = 5,    /* grouped down GEMM                         */
+    RMDA_STAGE_COMBINE = 6, /* weighted gather-sum (+ shared expert)     */
+    RMDA_PROF_STAGES = 7
+};
+
+/* Start accumulating per-stage GPU time of every later rmda_moe_layer call:
+ * a hipEvent is recorded on the context stream before the first stage and
+ * after each stage (created once, here; never in the layer call).  Every
+ * RMDA_PROF_RING layer calls the events are harvested, which waits for the
+ * stream: profiled runs are for measurement only. */
+#define RMDA_PROF_RING 64u
+int rmda_moe_prof_begin(rmda_moe_ctx_t *ctx);
+/* Stop, wait for the stream, and return the summed milliseconds per stage
+ * (ms[RMDA_PROF_STAGES]) and the number of layer calls they cover. */
+int rmda_moe_prof_end(rmda_moe_ctx_t *ctx, double *ms, uint32_t *layers);
+/* Name of stage i ("router", "route", ...), or NULL. */
+const char *rmda_moe_prof_stage_name(uint32_t i);
+
 /* ---- synthetic inputs (bench and tests) ---- */
 
 /* dst[i] = fp16 / fp32 of std * z_i where z_i is the standardised

@@ -20,6 +20,13 @@ struct rmda_moe_ctx {
     uint32_t *hist;
     uint32_t *done;
     uint32_t scatter_experts;
+    // stage profiler: a ring of per-call event sets, harvested when full
+    int prof_on;
+    int prof_made;
+    uint32_t prof_pending;
+    uint32_t prof_layers;
+    double prof_ms[RMDA_PROF_STAGES];
+    hipEvent_t prof_ev[RMDA_PROF_RING][RMDA_PROF_STAGES + 1];
 };
 
 namespace {
@@ -63,6 +70,38 @@ int hip_check(rmda_moe_ctx_t *c, hipError_t e, const char *what) {
 
 size_t align256(size_t x) {
     return (x + 255) & ~(size_t)255;
+}
+
+const char *const kStageNames[RMDA_PROF_STAGES] = {"router", "route", "rank", "permute",
+                                                   "gate_up", "down", "combine"};
+
+// Wait for the last recorded event set and fold every pending call's stage
+// intervals into the running sums (mda_vkc_prof_collect, src/vkc.c:617-628).
+int prof_harvest(rmda_moe_ctx_t *c) {
+    if (c->prof_pending == 0) {
+        return RMDA_OK;
+    }
+    int rc = hip_check(c, hipEventSynchronize(c->prof_ev[c->prof_pending - 1][RMDA_PROF_STAGES]),
+                       "profiler hipEventSynchronize");
+    for (uint32_t i = 0; i < c->prof_pending && rc == RMDA_OK; i += 1) {
+        for (uint32_t st = 0; st < RMDA_PROF_STAGES && rc == RMDA_OK; st += 1) {
+            float ms = 0.0f;
+            rc = hip_check(c, hipEventElapsedTime(&ms, c->prof_ev[i][st], c->prof_ev[i][st + 1]),
+                           "profiler hipEventElapsedTime");
+            c->prof_ms[st] += ms;
+        }
+    }
+    c->prof_layers += c->prof_pending;
+    c->prof_pending = 0;
+    return rc;
+}
+
+// Record the event that closes stage `st - 1` (st = 0 opens the call).
+int prof_mark(rmda_moe_ctx_t *c, uint32_t st) {
+    if (!c->prof_on) {
+        return RMDA_OK;
+    }
+    return hip_check(c, hipEventRecord(c->prof_ev[c->prof_pending][st], c->stream), "profiler hipEventRecord");
 }
 
 struct LayerPlan {
@@ -201,7 +240,67 @@ void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(ctx->scratch);
+    if (ctx->prof_made) {
+        for (uint32_t i = 0; i < RMDA_PROF_RING; i += 1) {
+            for (uint32_t st = 0; st <= RMDA_PROF_STAGES; st += 1) {
+                (void)hipEventDestroy(ctx->prof_ev[i][st]);
+            }
+        }
+    }
     delete ctx;
+}
+
+int rmda_moe_prof_begin(rmda_moe_ctx_t *ctx) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (!ctx->prof_made) {
+        for (uint32_t i = 0; i < RMDA_PROF_RING && rc == RMDA_OK; i += 1) {
+            for (uint32_t st = 0; st <= RMDA_PROF_STAGES && rc == RMDA_OK; st += 1) {
+                rc = hip_check(ctx, hipEventCreate(&ctx->prof_ev[i][st]), "profiler hipEventCreate");
+            }
+        }
+        if (rc != RMDA_OK) {
+            return rc;
+        }
+        ctx->prof_made = 1;
+    }
+    ctx->prof_on = 1;
+    ctx->prof_pending = 0;
+    ctx->prof_layers = 0;
+    for (uint32_t st = 0; st < RMDA_PROF_STAGES; st += 1) {
+        ctx->prof_ms[st] = 0.0;
+    }
+    return RMDA_OK;
+}
+
+int rmda_moe_prof_end(rmda_moe_ctx_t *ctx, double *ms, uint32_t *layers) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (!ctx->prof_on) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_prof_end: profiler not started");
+    }
+    rc = prof_harvest(ctx);
+    ctx->prof_on = 0;
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    for (uint32_t st = 0; st < RMDA_PROF_STAGES; st += 1) {
+        if (ms != nullptr) {
+            ms[st] = ctx->prof_ms[st];
+        }
+    }
+    if (layers != nullptr) {
+        *layers = ctx->prof_layers;
+    }
+    return RMDA_OK;
+}
+
+const char *rmda_moe_prof_stage_name(uint32_t i) {
+    return i < RMDA_PROF_STAGES ? kStageNames[i] : nullptr;
 }
 
 int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream) {
@@ -546,14 +645,29 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     uint16_t *hp = at<uint16_t>(ws, p.hp);
     uint16_t *ye = at<uint16_t>(ws, p.ye);
 
+    if (ctx->prof_on && ctx->prof_pending == RMDA_PROF_RING) {
+        rc = prof_harvest(ctx);
+        if (rc != RMDA_OK) {
+            return rc;
+        }
+    }
+    rc = prof_mark(ctx, 0);
     // A0 router projection (+ zero the rank ticket for this call)
-    rc = hip_check(ctx,
-                   rmda_launch_router(s, args->x, args->w_router, args->bias, proj, T, d, p.ps, p.ps,
-                                      args->bias != nullptr ? E : 0, done, 1),
-                   "layer router");
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx,
+                       rmda_launch_router(s, args->x, args->w_router, args->bias, proj, T, d, p.ps, p.ps,
+                                          args->bias != nullptr ? E : 0, done, 1),
+                       "layer router");
+    }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_ROUTER + 1);
+    }
     // A1 top-k
     if (rc == RMDA_OK) {
         rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
+    }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_ROUTE + 1);
     }
     // A2 counts, offsets, block bases and the GEMM work list
     if (rc == RMDA_OK) {
@@ -574,12 +688,18 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.shared_row0 = p.npairs;
         rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
     }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_RANK + 1);
+    }
     // A3 permutation (slots + row -> token map; x is gathered, not copied)
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
                        rmda_launch_permute(s, idx, lrank, at<uint32_t>(ws, p.hist), p.npairs, K, E, slot, rowtok,
                                            nullptr, nullptr, 0),
                        "layer permute");
+    }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_PERMUTE + 1);
     }
     rmda_gemm_args_t g{};
     g.items = at<uint32_t>(ws, p.items);
@@ -605,6 +725,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.ldo = I;
         rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer gate_up");
     }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_GATE_UP + 1);
+    }
     // A7 down -> ye16 (the shared expert's rows follow the routed rows)
     if (rc == RMDA_OK) {
         g.mode = RMDA_GEMM_F16;
@@ -621,12 +744,21 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.ldo = d;
         rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer down");
     }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_DOWN + 1);
+    }
     // A8/A9 combine (+ sigmoid-gated shared expert)
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
                        rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.npairs, shape->shared > 0, args->out,
                                              T, d, K),
                        "layer combine");
+    }
+    if (rc == RMDA_OK) {
+        rc = prof_mark(ctx, RMDA_STAGE_COMBINE + 1);
+    }
+    if (rc == RMDA_OK && ctx->prof_on) {
+        ctx->prof_pending += 1;
     }
     return rc;
 }

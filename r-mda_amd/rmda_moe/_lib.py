@@ -28,6 +28,8 @@ MAX_EXPERTS = 512
 MAX_TOPK = 16
 MM_TILE = 128
 CTX_MAX_PAIRS = 1 << 21
+PROF_STAGES = 7
+PROF_RING = 64
 
 
 class RoutePC(ctypes.Structure):
@@ -110,6 +112,9 @@ SIGNATURES = {
     "rmda_moe_workspace_bytes": (ctypes.c_size_t, [_p]),
     "rmda_moe_workspace_layout": (ctypes.c_int, [_p, _p]),
     "rmda_moe_layer": (ctypes.c_int, [_p, _p, _p]),
+    "rmda_moe_prof_begin": (ctypes.c_int, [_p]),
+    "rmda_moe_prof_end": (ctypes.c_int, [_p, _p, _p]),
+    "rmda_moe_prof_stage_name": (ctypes.c_char_p, [_u32]),
     "rmda_moe_fill_normal_f16": (ctypes.c_int, [_p, _p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
                                                 ctypes.c_float]),
     "rmda_moe_fill_normal_f32": (ctypes.c_int, [_p, _p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,

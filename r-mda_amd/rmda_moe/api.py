@@ -177,6 +177,19 @@ class Context:
                          workspace.numel() * workspace.element_size())
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
 
+    # ---- stage profiler ----
+
+    def prof_begin(self):
+        self._check(self.L.rmda_moe_prof_begin(self.h))
+
+    def prof_end(self):
+        """Stop profiling; returns ({stage: summed ms}, layer calls covered)."""
+        ms = (ctypes.c_double * _lib.PROF_STAGES)()
+        n = ctypes.c_uint32()
+        self._check(self.L.rmda_moe_prof_end(self.h, ms, ctypes.byref(n)))
+        names = [self.L.rmda_moe_prof_stage_name(i).decode() for i in range(_lib.PROF_STAGES)]
+        return dict(zip(names, list(ms))), n.value
+
     def fill_normal(self, t, stream, seed, std):
         if t.dtype == torch.float16:
             self._check(self.L.rmda_moe_fill_normal_f16(self.h, _ptr(t), t.numel(), stream, seed, std))
