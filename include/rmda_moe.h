@@ -282,6 +282,8 @@ typedef struct rmda_moe_layer_args_t {
     uint16_t *out;              /* rows x d fp16 */
     void *workspace;            /* >= rmda_moe_workspace_bytes(shape) bytes */
     size_t workspace_bytes;
+    const uint16_t *packed;     /* weights from rmda_moe_pack_weights, or NULL: then
+                                   the GEMMs read w_gate_up / w_down / w_sh_* */
 } rmda_moe_layer_args_t;
 
 /* Device views into the workspace after rmda_moe_layer (byte offsets), so a
@@ -310,6 +312,28 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
  * inter % 64 == 0, shared % 64 == 0, experts <= 512, topk <= 16. */
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
                    const rmda_moe_layer_args_t *args);
+
+/* ---- expert-weight packing (replaces the per-layer weight conversion at
+ * upload, src/qwen.c:376-394: qwen_bf16 converts the bf16 expert weights to
+ * fp16 in place after each layer's upload) ---- */
+
+/* Bytes of one layer's packed expert weights: routed gate_up and down, then
+ * the shared expert's gate_up and down when shape->shared > 0 (fp16, same
+ * element count as the HF tensors).  0 when the shape is rejected. */
+size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape);
+
+/* Reorder the HF-layout expert weights (w_gate_up [E][2I][d], w_down
+ * [E][d][I], and w_sh_gate_up [2I_s][d], w_sh_down [d][I_s] when shared > 0)
+ * into the order the grouped GEMM streams them: each 128-row x K-step slab
+ * becomes one contiguous block in exactly the layout the kernel keeps it in
+ * LDS, so every weight load is a contiguous KiB.  With bf16 != 0 the inputs
+ * are bf16 and are converted to fp16 (round to nearest even) on the way, in
+ * place of qwen_bf16.  Enqueued on the context stream; `packed` must hold
+ * rmda_moe_packed_bytes(shape) bytes and must not overlap the inputs.  A
+ * packed buffer is valid for contexts of the same library build. */
+int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const uint16_t *w_gate_up,
+                          const uint16_t *w_down, const uint16_t *w_sh_gate_up, const uint16_t *w_sh_down,
+                          int bf16, uint16_t *packed);
 
 /* ---- stage profiler (replaces the reference's timestamp profiler:
  * mda_vkc_prof_begin / mda_vkc_prof_mark / mda_vkc_prof_report,

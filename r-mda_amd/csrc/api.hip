@@ -5,6 +5,7 @@
 // (src/qwen.c:770-907).  Every call only enqueues work on the context stream.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "common.h"
@@ -20,6 +21,8 @@ struct rmda_moe_ctx {
     uint32_t *hist;
     uint32_t *done;
     uint32_t scatter_experts;
+    // grouped-GEMM configuration (RMDA_MOE_GEMM_VARIANT overrides; tuning only)
+    rmda_gemm2_cfg_t g2;
     // stage profiler: a ring of per-call event sets, harvested when full
     int prof_on;
     int prof_made;
@@ -146,7 +149,7 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.npairs = T * K;
     p.nblocks = p.npairs == 0 ? 1 : (p.npairs + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
     p.sh_rows = s->shared > 0 ? T : 0;
-    p.max_items = p.npairs / RMDA_GEMM_BM + E + (p.sh_rows + RMDA_GEMM_BM - 1) / RMDA_GEMM_BM;
+    p.max_items = p.npairs / RMDA_GEMM2_BM + E + (p.sh_rows + RMDA_GEMM2_BM - 1) / RMDA_GEMM2_BM;
     p.groups_rows = p.npairs + p.sh_rows;
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -169,6 +172,22 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.hp = take((size_t)p.groups_rows * s->inter * 2);
     p.ye = take((size_t)p.groups_rows * s->d * 2);
     p.total = o;
+    return p;
+}
+
+// element offsets (halves) of the four weight sets inside a packed buffer
+struct PackPlan {
+    size_t gate_up, down, sh_gate_up, sh_down, total;
+};
+
+PackPlan plan_pack(const rmda_moe_shape_t *s) {
+    PackPlan p{};
+    const size_t d = s->d;
+    p.gate_up = 0;
+    p.down = p.gate_up + (size_t)s->experts * 2 * s->inter * d;
+    p.sh_gate_up = p.down + (size_t)s->experts * d * s->inter;
+    p.sh_down = p.sh_gate_up + (size_t)2 * s->shared * d;
+    p.total = p.sh_down + d * s->shared;
     return p;
 }
 
@@ -226,6 +245,10 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
         return RMDA_ERR_HIP;
     }
     c->scatter_experts = 0;
+    c->g2 = rmda_gemm2_variant(0);
+    if (const char *v = getenv("RMDA_MOE_GEMM_VARIANT")) {
+        c->g2 = rmda_gemm2_variant(atoi(v));
+    }
     if (prev >= 0 && prev != device) {
         (void)hipSetDevice(prev);
     }
@@ -609,15 +632,16 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         return rc;
     }
     if (shape == nullptr || args == nullptr || args->x == nullptr || args->w_router == nullptr ||
-        args->w_gate_up == nullptr || args->w_down == nullptr || args->out == nullptr ||
-        args->workspace == nullptr) {
+        (args->packed == nullptr && (args->w_gate_up == nullptr || args->w_down == nullptr)) ||
+        args->out == nullptr || args->workspace == nullptr) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: null argument");
     }
     char why[128];
     if (!check_shape(shape, why, sizeof(why))) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_layer: %s", why);
     }
-    if (shape->shared > 0 && (args->w_sh_gate_up == nullptr || args->w_sh_down == nullptr)) {
+    if (shape->shared > 0 && args->packed == nullptr &&
+        (args->w_sh_gate_up == nullptr || args->w_sh_down == nullptr)) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: shared expert weights missing");
     }
     const LayerPlan p = plan_layer(shape);
@@ -644,6 +668,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     uint32_t *done = at<uint32_t>(ws, p.done);
     uint16_t *hp = at<uint16_t>(ws, p.hp);
     uint16_t *ye = at<uint16_t>(ws, p.ye);
+    const uint16_t *packed = args->packed;
+    const PackPlan pk = plan_pack(shape);
+    const uint16_t *w_gu = packed != nullptr ? packed + pk.gate_up : args->w_gate_up;
+    const uint16_t *w_dn = packed != nullptr ? packed + pk.down : args->w_down;
+    const uint16_t *w_sgu = packed != nullptr ? packed + pk.sh_gate_up : args->w_sh_gate_up;
+    const uint16_t *w_sdn = packed != nullptr ? packed + pk.sh_down : args->w_sh_down;
 
     if (ctx->prof_on && ctx->prof_pending == RMDA_PROF_RING) {
         rc = prof_harvest(ctx);
@@ -683,7 +713,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.done = done;
         ra.items = at<uint32_t>(ws, p.items);
         ra.n_items = at<uint32_t>(ws, p.n_items);
-        ra.bm = RMDA_GEMM_BM;
+        ra.bm = RMDA_GEMM2_BM;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.npairs;
         rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
@@ -715,15 +745,15 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.a = args->x;
         g.rowtok = rowtok;
         g.lda = d;
-        g.w = args->w_gate_up;
-        g.w_shared = args->w_sh_gate_up;
+        g.w = w_gu;
+        g.w_shared = w_sgu;
         g.n_w = 2 * I;
         g.k = d;
         g.n_out = I;
         g.inter = I;
         g.out = hp;
         g.ldo = I;
-        rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer gate_up");
+        rc = hip_check(ctx, rmda_launch_gemm2(s, &g, ctx->g2, packed != nullptr), "layer gate_up");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_GATE_UP + 1);
@@ -734,15 +764,15 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.a = hp;
         g.rowtok = nullptr;
         g.lda = I;
-        g.w = args->w_down;
-        g.w_shared = args->w_sh_down;
+        g.w = w_dn;
+        g.w_shared = w_sdn;
         g.n_w = d;
         g.k = I;
         g.n_out = d;
         g.inter = 0;
         g.out = ye;
         g.ldo = d;
-        rc = hip_check(ctx, rmda_launch_gemm(s, &g), "layer down");
+        rc = hip_check(ctx, rmda_launch_gemm2(s, &g, ctx->g2, packed != nullptr), "layer down");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_DOWN + 1);
@@ -759,6 +789,52 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     }
     if (rc == RMDA_OK && ctx->prof_on) {
         ctx->prof_pending += 1;
+    }
+    return rc;
+}
+
+size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape) {
+    if (shape == nullptr) {
+        return 0;
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return 0;
+    }
+    return plan_pack(shape).total * 2;
+}
+
+int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const uint16_t *w_gate_up,
+                          const uint16_t *w_down, const uint16_t *w_sh_gate_up, const uint16_t *w_sh_down, int bf16,
+                          uint16_t *packed) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (shape == nullptr || w_gate_up == nullptr || w_down == nullptr || packed == nullptr ||
+        (shape->shared > 0 && (w_sh_gate_up == nullptr || w_sh_down == nullptr))) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_pack_weights: null argument");
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_pack_weights: %s", why);
+    }
+    const PackPlan pk = plan_pack(shape);
+    const uint32_t E = shape->experts, d = shape->d, I = shape->inter, S = shape->shared;
+    const int bk = (int)ctx->g2.bk;
+    hipStream_t s = ctx->stream;
+    rc = hip_check(ctx, rmda_launch_pack(s, w_gate_up, packed + pk.gate_up, E, 2 * I, d, I, 1, bk, bf16),
+                   "pack gate_up");
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_pack(s, w_down, packed + pk.down, E, d, I, I, 0, bk, bf16), "pack down");
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = hip_check(ctx, rmda_launch_pack(s, w_sh_gate_up, packed + pk.sh_gate_up, 1, 2 * S, d, S, 1, bk, bf16),
+                       "pack shared gate_up");
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = hip_check(ctx, rmda_launch_pack(s, w_sh_down, packed + pk.sh_down, 1, d, S, S, 0, bk, bf16),
+                       "pack shared down");
     }
     return rc;
 }

@@ -124,6 +124,24 @@ struct rmda_gemm_args_t {
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 #define RMDA_GEMM_BM 128u
 
+// gemm2.hip: the fused layer's grouped GEMM (SWIGLU and F16 modes) over
+// work items of up to RMDA_GEMM2_BM rows, reading HF-layout or packed
+// weights.  A configuration is (N tile, K step, pipeline depth); variant
+// numbers name the ones built (rmda_gemm2_variant; 0 = default).  Requires
+// n_w % 128 == 0 and k % bk == 0.
+#define RMDA_GEMM2_BM 256u
+struct rmda_gemm2_cfg_t {
+    uint32_t bn;
+    uint32_t bk;
+    uint32_t stages;
+};
+rmda_gemm2_cfg_t rmda_gemm2_variant(int variant);
+hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm2_cfg_t c, int packed);
+// Reorder `groups` row-major [n_w][k] matrices (fp16, or bf16 when bf16_in)
+// into the packed slab order of K step bk (SWIGLU: gate/up interleave).
+hipError_t rmda_launch_pack(hipStream_t s, const uint16_t *src, uint16_t *dst, uint32_t groups, uint32_t n_w,
+                            uint32_t k, uint32_t inter, int swiglu, int bk, int bf16_in);
+
 // combine.hip
 hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, const float *wt,
                                const uint32_t *slot, const float *y, const float *proj,

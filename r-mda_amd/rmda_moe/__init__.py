@@ -13,7 +13,7 @@ __all__ = ["configs", "lib", "LIB_PATH", "NONE", "NO_SLOT", "header_functions", 
 
 def __getattr__(name):
     # torch is imported lazily so host-only helpers work without it
-    if name in ("Context", "MoeError", "workspace_bytes", "workspace_layout", "ws_views"):
+    if name in ("Context", "MoeError", "workspace_bytes", "workspace_layout", "ws_views", "packed_bytes"):
         from . import api
         return getattr(api, name)
     raise AttributeError(name)

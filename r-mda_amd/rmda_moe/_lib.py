@@ -78,7 +78,7 @@ class Shape(ctypes.Structure):
 class LayerArgs(ctypes.Structure):
     _fields_ = [("x", _p), ("w_router", _p), ("bias", _p), ("w_gate_up", _p), ("w_down", _p),
                 ("w_sh_gate_up", _p), ("w_sh_down", _p), ("out", _p), ("workspace", _p),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("packed", _p)]
 
 
 class WsLayout(ctypes.Structure):
@@ -112,6 +112,8 @@ SIGNATURES = {
     "rmda_moe_workspace_bytes": (ctypes.c_size_t, [_p]),
     "rmda_moe_workspace_layout": (ctypes.c_int, [_p, _p]),
     "rmda_moe_layer": (ctypes.c_int, [_p, _p, _p]),
+    "rmda_moe_packed_bytes": (ctypes.c_size_t, [_p]),
+    "rmda_moe_pack_weights": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, ctypes.c_int, _p]),
     "rmda_moe_prof_begin": (ctypes.c_int, [_p]),
     "rmda_moe_prof_end": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_prof_stage_name": (ctypes.c_char_p, [_u32]),

@@ -49,6 +49,12 @@ def workspace_bytes(shape):
     return _lib.lib().rmda_moe_workspace_bytes(ctypes.byref(s))
 
 
+def packed_bytes(shape):
+    """rmda_moe_packed_bytes; 0 means the shape is rejected.  Host-only."""
+    s = shape_struct(shape)
+    return _lib.lib().rmda_moe_packed_bytes(ctypes.byref(s))
+
+
 def workspace_layout(shape):
     s = shape_struct(shape)
     lay = WsLayout()
@@ -170,12 +176,26 @@ class Context:
 
     # ---- fused layer ----
 
-    def layer(self, shape, x, w_router, bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down, out, workspace):
+    def layer(self, shape, x, w_router, bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down, out, workspace,
+              packed=None):
         s = shape_struct(shape)
         args = LayerArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(w_gate_up), _ptr(w_down),
                          _ptr(w_sh_gate_up), _ptr(w_sh_down), _ptr(out), _ptr(workspace),
-                         workspace.numel() * workspace.element_size())
+                         workspace.numel() * workspace.element_size(), _ptr(packed))
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
+
+    def pack_weights(self, shape, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, bf16=False, packed=None):
+        """rmda_moe_pack_weights into `packed` (allocated when None); returns it."""
+        if packed is None:
+            n = packed_bytes(shape)
+            if n == 0:
+                raise ValueError("shape rejected by rmda_moe_packed_bytes: %r" % (shape,))
+            packed = torch.empty(n // 2, dtype=torch.float16, device=w_gate_up.device)
+        s = shape_struct(shape)
+        self._check(self.L.rmda_moe_pack_weights(self.h, ctypes.byref(s), _ptr(w_gate_up), _ptr(w_down),
+                                                 _ptr(w_sh_gate_up), _ptr(w_sh_down), 1 if bf16 else 0,
+                                                 _ptr(packed)))
+        return packed
 
     # ---- stage profiler ----
 

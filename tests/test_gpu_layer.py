@@ -27,12 +27,16 @@ def ctx():
     c.close()
 
 
-def run_layer(ctx, inp):
+def run_layer(ctx, inp, packed=None):
     shape = inp["shape"]
     ws = inputs.workspace_for(shape)
     out = torch.full((shape["rows"], shape["d"]), float("nan"), dtype=torch.float16, device="cuda")
-    ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
-              inp["w_sh_gate_up"], inp["w_sh_down"], out, ws)
+    if packed is None:
+        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
+                  inp["w_sh_gate_up"], inp["w_sh_down"], out, ws)
+    else:
+        # packed weights only: the HF-layout pointers are not passed
+        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed)
     ctx.sync()
     return out, api.ws_views(shape, ws)
 
@@ -60,6 +64,10 @@ def check_layer(ctx, cfg, seed, n_sample=None):
     max_abs, rel = out_metrics(got, ref["out"])
     print("  max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+    # packed weights feed the MFMAs the same LDS images: bitwise the same output
+    packed = ctx.pack_weights(inp["shape"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"], inp["w_sh_down"])
+    out_p, _ = run_layer(ctx, inp, packed=packed)
+    assert torch.equal(out_p.view(torch.int16), out.view(torch.int16)), "packed-weight output differs"
     return out
 
 
@@ -95,3 +103,26 @@ def test_layer_skew_has_empty_experts(ctx):
     cnt = u32(views["count"])
     assert (cnt == 0).sum() > 0, "config 4 is meant to leave some experts empty"
     assert cnt.sum() == cfg["rows"] * cfg["topk"]
+
+
+def test_pack_bf16_input_equals_fp16_of_converted(ctx):
+    """bf16 packing converts like qwen_bf16 (round to nearest even), then packs."""
+    cfg = dict(configs.CONFIGS[1], rows=64, name="bf16")
+    shape = configs.shape_of(cfg)
+    E, d, I = shape["experts"], shape["d"], shape["inter"]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    gu = (torch.randn(E, 2 * I, d, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    dn = (torch.randn(E, d, I, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    p_bf = ctx.pack_weights(shape, gu.view(torch.float16), dn.view(torch.float16), bf16=True)
+    # reference conversion through the oracle's qwen_bf16 restatement
+    gu16 = orc.qwen_bf16(gu.view(torch.int32).cpu().numpy().view(np.uint32))
+    dn16 = orc.qwen_bf16(dn.view(torch.int32).cpu().numpy().view(np.uint32))
+    gu_h = torch.from_numpy(gu16.view(np.int16)).cuda().view(torch.float16).view(E, 2 * I, d)
+    dn_h = torch.from_numpy(dn16.view(np.int16)).cuda().view(torch.float16).view(E, d, I)
+    p_h = ctx.pack_weights(shape, gu_h, dn_h)
+    ctx.sync()
+    assert torch.equal(p_bf.view(torch.int16), p_h.view(torch.int16))
+    # packing is a permutation of the elements
+    a = np.sort(p_h.view(torch.int16).cpu().numpy().ravel())
+    b = np.sort(np.concatenate([gu16.view(np.int16).ravel(), dn16.view(np.int16).ravel()]))
+    assert np.array_equal(a, b)
