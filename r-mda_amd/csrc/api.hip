@@ -162,7 +162,7 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.wt = take((size_t)p.npairs * 4);
     p.lrank = take((size_t)p.npairs * 4);
     p.slot = take((size_t)p.npairs * 4);
-    p.rowtok = take((size_t)p.npairs * 4);
+    p.rowtok = take((size_t)(p.npairs + RMDA_ROWTOK_PAD) * 4);
     p.count = take((size_t)E * 4);
     p.off = take((size_t)E * 4);
     p.hist = take((size_t)p.nblocks * E * 4);
@@ -249,6 +249,7 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
     if (const char *v = getenv("RMDA_MOE_GEMM_VARIANT")) {
         c->g2 = rmda_gemm2_variant(atoi(v));
     }
+    c->g2.grid = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 256u;
     if (prev >= 0 && prev != device) {
         (void)hipSetDevice(prev);
     }

@@ -129,12 +129,16 @@ hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 // weights.  A configuration is (N tile, K step, pipeline depth); variant
 // numbers name the ones built (rmda_gemm2_variant; 0 = default).  Requires
 // n_w % 128 == 0 and k % bk == 0.
-#define RMDA_GEMM2_BM 256u
+#define RMDA_GEMM2_BM 192u
 struct rmda_gemm2_cfg_t {
     uint32_t bn;
     uint32_t bk;
     uint32_t stages;
+    uint32_t grid;  // persistent workgroups (the device's CU count)
 };
+// rows of padding after the gathered-row index buffer (rowtok) that the
+// grouped GEMM's scalar index reads may touch
+#define RMDA_ROWTOK_PAD 256u
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant);
 hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm2_cfg_t c, int packed);
 // Reorder `groups` row-major [n_w][k] matrices (fp16, or bf16 when bf16_in)

@@ -40,9 +40,8 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr uint32_t BM = RMDA_GEMM2_BM;  // 256 rows per work item
+constexpr uint32_t BM = RMDA_GEMM2_BM;  // rows per work item (three 64-row blocks)
 constexpr uint32_t SLAB = 128;          // packed slab height (B rows)
-constexpr uint32_t NT = 512;
 
 // chunk swizzle of row r (BK/8 chunks per row): chunk c of row r sits in
 // slot c ^ ((r >> 1) & (BK/8 - 1)).  Chosen by measurement on gfx950
@@ -79,244 +78,390 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// wait until this wave's loads of the oldest pending stage have landed;
-// `after` = later stages already issued (0 .. STAGES-2)
-template <int LOADS, int STAGES>
-__device__ __forceinline__ void wait_stage(uint32_t after) {
-    if constexpr (STAGES >= 4) {
-        if (after >= 2) {
-            wait_vm<2 * LOADS>();
-            return;
-        }
+// wait until this wave's loads of the oldest pending stage have landed:
+// `after` later stages (0 .. 4) of L loads each may stay in flight
+template <int L>
+__device__ __forceinline__ void wait_after(uint32_t after) {
+    switch (after) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<L>(); break;
+    case 2: wait_vm<2 * L>(); break;
+    case 3: wait_vm<3 * L>(); break;
+    default: wait_vm<4 * L>(); break;
     }
-    if constexpr (STAGES >= 3) {
-        if (after >= 1) {
-            wait_vm<LOADS>();
-            return;
-        }
-    }
-    wait_vm<0>();
 }
 
+// `loads` is one of the four per-wave stage sizes (uniform per wave)
+template <int LA, int LB_HI, int LB_LO>
+__device__ __forceinline__ void wait_stage(bool live, bool b_hi, uint32_t after) {
+    if (live) {
+        if (b_hi) {
+            wait_after<LA + LB_HI>(after);
+        } else {
+            wait_after<LA + LB_LO>(after);
+        }
+    } else {
+        if (b_hi) {
+            wait_after<LB_HI>(after);
+        } else {
+            wait_after<LB_LO>(after);
+        }
+    }
+}
+
+// Persistent workgroup: MB (=3) blocks of 64 rows x BN/64 (=4) column
+// blocks of 64, one wave each (12 waves).  Waves w and w + 4 share a SIMD, so
+// the four waves of a row block sit on four different SIMDs and any number of
+// live row blocks keeps the SIMDs balanced.
+//
+// One workgroup per CU walks a strided list of (work item, N tile) tasks.
+// All tasks of a launch have the same K, so the workgroup's stages form one
+// stream: stage g is K step g % steps of its task g / steps, and the ring
+// keeps STAGES-1 stages in flight across task boundaries (the next task's
+// first stages load while the current one finishes and stores its tile).
+// Task descriptors and gathered row indices come in through scalar loads
+// (constant address space, counted by lgkmcnt), so the vmcnt bookkeeping of
+// the ring sees nothing but the stage loads: every wave issues the same
+// number of loads per stage (A rows of idle row blocks re-read row 0), and
+// the stores of a finished tile are never counted in a wait's allowance, so
+// each wait is exact or conservative.
+typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
+
 template <int MODE, int BN, int BK, int STAGES, bool PACKED>
-__global__ __launch_bounds__(512) void gemm2_kernel(rmda_gemm_args_t g) {
+__global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
+    constexpr uint32_t MB = BM / 64;             // row blocks
+    constexpr uint32_t NB = BN / 64;             // column blocks
+    constexpr uint32_t NWAVES = MB * NB;
     constexpr uint32_t CH = BK / 8;              // 16-byte chunks per row
     constexpr uint32_t RPI = 64 / CH;            // rows per wave-wide DMA instruction
     constexpr uint32_t A_BYTES = BM * BK * 2;
     constexpr uint32_t B_BYTES = BN * BK * 2;
     constexpr uint32_t STAGE_BYTES = A_BYTES + B_BYTES;
-    constexpr uint32_t A_INSTR = 32 / RPI;       // per live wave per stage (32 A rows)
-    constexpr uint32_t B_INSTR = BN / RPI / 8;   // per wave per stage
-    constexpr int LOADS_LIVE = (int)(A_INSTR + B_INSTR);
-    constexpr int LOADS_IDLE = (int)B_INSTR;
-    constexpr uint32_t WN = BN / 2;              // B rows per wave
-    constexpr uint32_t NJ = WN / 16;             // 16-wide MFMA column blocks per wave
+    constexpr uint32_t AW = 64 / NB;             // A rows loaded per wave
+    constexpr uint32_t A_PER = AW / RPI;         // A instructions per wave per stage
+    constexpr uint32_t B_ALL = BN / RPI;         // B instructions per stage, dealt round-robin
+    constexpr uint32_t B_HI = (B_ALL + NWAVES - 1) / NWAVES;
+    constexpr uint32_t B_LO = B_ALL / NWAVES;
+    static_assert(A_PER >= 1 && AW % RPI == 0 && AW <= 16, "A rows per wave must fill DMA instructions");
+    static_assert(STAGES >= 2 && STAGES <= 6, "pipeline depth");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
-    // waves are placed on SIMD w % 4: pairing (wm, wn) as (w / 2, w % 2) puts
-    // the two live waves of a 64-row block on different SIMDs and spreads the
-    // live blocks of a short item over all four
-    const uint32_t wm = w / 2;
-    const uint32_t wn = w % 2;
+    const uint32_t wm = w / NB;
+    const uint32_t wn = w % NB;
 
-    // ---- work assignment: balanced, XCD-contiguous over the real work ----
+    // ---- this workgroup's tasks: XCD x owns a contiguous, equal share ----
+    const_u32p items = (const_u32p)g.items;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
-    const uint32_t n_items = g.n_items != nullptr ? *g.n_items : g.max_items;
+    const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
     const uint32_t total = n_items * ntiles;
     const uint32_t per = (total + 7) / 8;
-    const uint32_t pos = blockIdx.x / 8;
-    if (pos >= per) {
+    const uint32_t xcd = blockIdx.x % 8;
+    const uint32_t stride = gridDim.x / 8;
+    const uint32_t first = xcd * per + blockIdx.x / 8;
+    const uint32_t last = min((xcd + 1) * per, total);
+    if (first >= last) {
         return;
     }
-    const uint32_t logical = (blockIdx.x % 8) * per + pos;
-    if (logical >= total) {
-        return;
-    }
-    const uint32_t item = logical / ntiles;
-    const uint32_t nt = logical % ntiles;
-    const uint4 it = reinterpret_cast<const uint4 *>(g.items)[item];
-    const uint32_t grp = it.x;
-    const uint32_t row0 = it.y;
-    const uint32_t rows = it.z;
-    const bool is_shared = grp == g.shared_group;
-    const uint16_t *wg = is_shared ? g.w_shared : g.w + (size_t)grp * g.n_w * g.k;
+    const uint32_t ntask = (last - first + stride - 1) / stride;
     const uint32_t steps = g.k / BK;
-    // a wave is live if some row of its 64-row block is (uniform per wave)
-    const bool live = wm * 64 < rows;
+    const uint32_t nstage = ntask * steps;
+    const bool b_hi = w < B_ALL % NWAVES || B_ALL % NWAVES == 0;
+    const uint32_t n_b = b_hi ? B_HI : B_LO;
 
-    // ---- per-lane DMA sources ----
     const uint32_t lrow = lane / CH;   // row within one instruction's block
     const uint32_t lch = lane % CH;    // LDS chunk slot
-    // A: wave (wm, wn) loads rows wm*64 + wn*32 + [0, 32); rows past the
-    // item's end re-read row 0 of the item
-    const uint16_t *a_src[A_INSTR];
-    uint32_t a_dst[A_INSTR];
+
+    // ---- issue side: per-lane DMA sources of the task being loaded ----
+    const uint16_t *a_src[A_PER];
+    uint32_t a_dst[A_PER];
+    const uint16_t *b_src[B_HI];
+    uint32_t b_dst[B_HI];
 #pragma unroll
-    for (uint32_t j = 0; j < A_INSTR; j += 1) {
-        const uint32_t rbase = wm * 64 + wn * 32 + j * RPI;
-        const uint32_t r = rbase + lrow;
-        const uint32_t rr = r < rows ? r : 0u;
-        uint32_t arow;
-        if (MODE == RMDA_GEMM_SWIGLU) {
-            arow = is_shared ? row0 + rr - g.shared_row0 : g.rowtok[row0 + rr];
-        } else {
-            arow = row0 + rr;
-        }
-        a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
-        a_dst[j] = rbase * (BK * 2);
+    for (uint32_t j = 0; j < A_PER; j += 1) {
+        a_dst[j] = (wm * 64 + wn * AW + j * RPI) * (BK * 2);
     }
-    // B: wave w loads tile rows (w*B_INSTR + j)*RPI + [0, RPI)
-    const uint16_t *b_src[B_INSTR];
 #pragma unroll
-    for (uint32_t j = 0; j < B_INSTR; j += 1) {
-        const uint32_t nbase = (w * B_INSTR + j) * RPI;
-        const uint32_t slab = nt * (BN / SLAB) + nbase / SLAB;
-        const uint32_t nin = nbase % SLAB;
-        if (PACKED) {
-            b_src[j] = wg + (size_t)slab * steps * (SLAB * BK) + nin * BK + lane * 8;
-        } else {
-            const uint32_t n = nin + lrow;
-            b_src[j] = wg + (size_t)slab_row<MODE>(slab, n, g.inter) * g.k + (lch ^ swz<BK>(n)) * 8;
-        }
+    for (uint32_t j = 0; j < B_HI; j += 1) {
+        const uint32_t bi = j < n_b ? w + j * NWAVES : w;
+        b_dst[j] = A_BYTES + bi * RPI * (BK * 2);
     }
-    auto issue = [&](uint32_t s, uint32_t buf) {
-        uint8_t *base = smem + buf * STAGE_BYTES;
-        if (live) {
+    auto setup = [&](uint32_t k) __attribute__((always_inline)) {
+        const uint32_t task = first + k * stride;
+        const uint32_t item = task / ntiles;
+        const uint32_t nt = task % ntiles;
+        const uint32_t grp = items[item * 4 + 0];
+        const uint32_t row0 = items[item * 4 + 1];
+        const uint32_t rows = items[item * 4 + 2];
+        const bool is_shared = grp == g.shared_group;
+        const uint16_t *wg = is_shared ? g.w_shared : g.w + (size_t)grp * g.n_w * g.k;
+        // gathered token rows of this wave's AW A rows (scalar loads; the
+        // index buffer is padded so the 16-entry read never leaves it)
+        const uint32_t rbase = wm * 64 + wn * AW;
+        uint32_t tok[16];
+        uint32_t tok0 = 0;
+        if (MODE == RMDA_GEMM_SWIGLU && !is_shared) {
+            const const_u32p rt = (const_u32p)g.rowtok + row0;
+            tok0 = rt[0];
 #pragma unroll
-            for (uint32_t j = 0; j < A_INSTR; j += 1) {
-                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + s * BK), (lds_void_t *)(base + a_dst[j]),
-                                                 16, 0, 0);
+            for (uint32_t c = 0; c < 16; c += 1) {
+                tok[c] = rt[rbase + c];
             }
         }
 #pragma unroll
-        for (uint32_t j = 0; j < B_INSTR; j += 1) {
-            const uint16_t *src = PACKED ? b_src[j] + (size_t)s * (SLAB * BK) : b_src[j] + s * BK;
-            __builtin_amdgcn_global_load_lds((const void *)src,
-                                             (lds_void_t *)(base + A_BYTES + (w * B_INSTR + j) * 1024), 16, 0, 0);
+        for (uint32_t j = 0; j < A_PER; j += 1) {
+            const uint32_t rl = j * RPI + lrow;  // row within the wave's AW rows
+            const uint32_t r = rbase + rl;
+            const uint32_t rr = r < rows ? r : 0u;
+            uint32_t arow;
+            if (MODE == RMDA_GEMM_SWIGLU) {
+                if (is_shared) {
+                    arow = row0 + rr - g.shared_row0;
+                } else {
+                    uint32_t t = tok[0];
+#pragma unroll
+                    for (uint32_t c = 1; c < 16; c += 1) {
+                        t = rl == c ? tok[c] : t;
+                    }
+                    arow = r < rows ? t : tok0;
+                }
+            } else {
+                arow = row0 + rr;
+            }
+            a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < B_HI; j += 1) {
+            const uint32_t bi = j < n_b ? w + j * NWAVES : w;
+            const uint32_t nbase = bi * RPI;
+            const uint32_t slab = nt * (BN / SLAB) + nbase / SLAB;
+            const uint32_t nin = nbase % SLAB;
+            if (PACKED) {
+                b_src[j] = wg + (size_t)slab * steps * (SLAB * BK) + nin * BK + lane * 8;
+            } else {
+                const uint32_t n = nin + lrow;
+                b_src[j] = wg + (size_t)slab_row<MODE>(slab, n, g.inter) * g.k + (lch ^ swz<BK>(n)) * 8;
+            }
         }
     };
-
-    floatx4_t acc[4][NJ];
-#pragma unroll
-    for (int i = 0; i < 4; i += 1) {
-#pragma unroll
-        for (uint32_t j = 0; j < NJ; j += 1) {
-            acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    uint32_t i_task = 0;  // task ordinal and K step of the next stage to issue
+    uint32_t i_s = 0;
+    setup(0);
+    // The stage's DMA instructions are issued one at a time between MFMA
+    // groups (see the main loop), so the CU's load path is fed while the
+    // matrix pipe works instead of all waves stalling on it at once.
+    uint8_t *ibase = smem;
+    auto issue_begin = [&](uint32_t buf) __attribute__((always_inline)) {
+        if (i_s == steps) {
+            i_task += 1;
+            i_s = 0;
+            setup(i_task);
         }
-    }
+        ibase = smem + buf * STAGE_BYTES;
+    };
+    // instruction q of this wave's stage: A rows first, then its B slices
+    auto issue_one = [&](uint32_t q) __attribute__((always_inline)) {
+        if (q < A_PER) {
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[q] + i_s * BK), (lds_void_t *)(ibase + a_dst[q]), 16,
+                                             0, 0);
+        } else if (q - A_PER < n_b) {
+            const uint32_t j = q - A_PER;
+            const uint16_t *src = PACKED ? b_src[j] + (size_t)i_s * (SLAB * BK) : b_src[j] + i_s * BK;
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)(ibase + b_dst[j]), 16, 0, 0);
+        }
+    };
+    auto issue_end = [&]() __attribute__((always_inline)) { i_s += 1; };
+    auto issue_next = [&](uint32_t buf) __attribute__((always_inline)) {
+        issue_begin(buf);
+#pragma unroll
+        for (uint32_t q = 0; q < A_PER + B_HI; q += 1) {
+            issue_one(q);
+        }
+        issue_end();
+    };
 
-    // fragment addresses: lane reads row (block base + lane%16), chunk (kk*4 + lane/16)
+    // ---- compute side ----
     const uint32_t fr = lane % 16;
     const uint32_t fq = lane / 16;
-    uint32_t a_off[4][BK / 32];
-    uint32_t b_off[NJ][BK / 32];
+    uint32_t ch_off[BK / 32];
 #pragma unroll
     for (uint32_t kk = 0; kk < BK / 32; kk += 1) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i += 1) {
-            const uint32_t ra = wm * 64 + i * 16 + fr;
-            a_off[i][kk] = ra * (BK * 2) + (((kk * 4 + fq) ^ swz<BK>(ra)) * 16);
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < NJ; j += 1) {
-            const uint32_t rb = wn * WN + j * 16 + fr;
-            b_off[j][kk] = A_BYTES + rb * (BK * 2) + (((kk * 4 + fq) ^ swz<BK>(rb)) * 16);
-        }
+        ch_off[kk] = ((kk * 4 + fq) ^ swz<BK>(fr)) * 16;
     }
-
-#pragma unroll
-    for (uint32_t s = 0; s < STAGES - 1; s += 1) {
-        if (s < steps) {
-            issue(s, s);
-        }
-    }
-    for (uint32_t s = 0; s < steps; s += 1) {
-        const uint32_t left = steps - 1 - s;
-        const uint32_t after = left < STAGES - 2 ? left : STAGES - 2;
-        if (live) {
-            wait_stage<LOADS_LIVE, STAGES>(after);
-        } else {
-            wait_stage<LOADS_IDLE, STAGES>(after);
-        }
-        lds_barrier();
-        if (s + STAGES - 1 < steps) {
-            issue(s + STAGES - 1, (s + STAGES - 1) % STAGES);
-        }
-        if (live) {
-            const uint8_t *base = smem + (s % STAGES) * STAGE_BYTES;
-#pragma unroll
-            for (uint32_t kk = 0; kk < BK / 32; kk += 1) {
-                half8_t af[4];
-                half8_t bf[NJ];
-#pragma unroll
-                for (int i = 0; i < 4; i += 1) {
-                    af[i] = *reinterpret_cast<const half8_t *>(base + a_off[i][kk]);
-                }
-#pragma unroll
-                for (uint32_t j = 0; j < NJ; j += 1) {
-                    bf[j] = *reinterpret_cast<const half8_t *>(base + b_off[j][kk]);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i += 1) {
-#pragma unroll
-                    for (uint32_t j = 0; j < NJ; j += 1) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
-        }
-    }
-    if (!live) {
-        return;
-    }
-
-    // epilogue: acc[i][j][v] is C[wm*64 + i*16 + 4*(lane/16) + v][B row wn*WN + j*16 + lane%16]
+    const uint32_t a_row_off = (wm * 64 + fr) * (BK * 2);
+    const uint32_t b_row_off = A_BYTES + (wn * 64 + fr) * (BK * 2);
     const uint32_t rq = 4 * fq;
-    uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
-    if (MODE == RMDA_GEMM_F16) {
+    floatx4_t acc[4][4];
+    uint32_t c_row0 = 0;
+    uint32_t c_rows = 0;
+    uint32_t c_nt = 0;
+    uint32_t kc = 0;  // compute task ordinal and K step
+    uint32_t ks = 0;
+    bool live = false;
+    constexpr uint32_t KK = BK / 32;
+    typedef half8_t frag_t[KK][4];
+    frag_t fa0, fb0;
+    auto load_frags = [&](uint32_t buf, frag_t &fa, frag_t &fb) __attribute__((always_inline)) {
+        const uint8_t *base = smem + buf * STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < 4; i += 1) {
+        for (uint32_t kk = 0; kk < KK; kk += 1) {
 #pragma unroll
-            for (int v = 0; v < 4; v += 1) {
-                const uint32_t rr = wm * 64 + i * 16 + rq + v;
-                if (rr < rows) {
+            for (int i = 0; i < 4; i += 1) {
+                fa[kk][i] = *reinterpret_cast<const half8_t *>(base + a_row_off + i * 16 * (BK * 2) + ch_off[kk]);
+                fb[kk][i] = *reinterpret_cast<const half8_t *>(base + b_row_off + i * 16 * (BK * 2) + ch_off[kk]);
+            }
+        }
+    };
+    // one stage of MMA on fragments (fa, fb) in four groups of four MFMAs,
+    // with the task bookkeeping; `between(q)` runs after group q (q < 3)
+    auto compute_begin = [&]() __attribute__((always_inline)) {
+        if (ks == 0) {
+            const uint32_t task = first + kc * stride;
+            const uint32_t item = task / ntiles;
+            c_nt = task - item * ntiles;
+            c_row0 = items[item * 4 + 1];
+            c_rows = items[item * 4 + 2];
+            live = wm * 64 < c_rows;
 #pragma unroll
-                    for (uint32_t j = 0; j < NJ; j += 1) {
-                        const uint32_t col = nt * BN + wn * WN + j * 16 + fr;
-                        O[(size_t)(row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
-                    }
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
                 }
             }
         }
-    } else {
-        // within each 64-row group of B rows, blocks u (gate) and u + 2 (up)
-        // hold the same output columns
+    };
+    auto mfma_group = [&](const frag_t &fa, const frag_t &fb, int i) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i += 1) {
+        for (uint32_t kk = 0; kk < KK; kk += 1) {
 #pragma unroll
-            for (int v = 0; v < 4; v += 1) {
-                const uint32_t rr = wm * 64 + i * 16 + rq + v;
-                if (rr < rows) {
+            for (int j = 0; j < 4; j += 1) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+    auto compute_end = [&]() __attribute__((always_inline)) {
+        if (live && ks == steps - 1) {
+            // tile epilogue: acc[i][j][v] is
+            // C[wm*64 + i*16 + 4*(lane/16) + v][B row wn*64 + j*16 + lane%16]
+            uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
+            if (MODE == RMDA_GEMM_F16) {
 #pragma unroll
-                    for (uint32_t gq = 0; gq < NJ / 4; gq += 1) {
+                for (int i = 0; i < 4; i += 1) {
 #pragma unroll
-                        for (uint32_t u = 0; u < 2; u += 1) {
-                            const float gt = acc[i][gq * 4 + u][v];
-                            const float up = acc[i][gq * 4 + u + 2][v];
-                            const float h = gt / (1.0f + __expf(-gt)) * up;
-                            const uint32_t bl = wn * WN + gq * 64 + u * 16;  // local B row of the block
-                            const uint32_t slab = nt * (BN / SLAB) + bl / SLAB;
-                            const uint32_t col = slab * 64 + ((bl % SLAB) / 64) * 32 + u * 16 + fr;
-                            O[(size_t)(row0 + rr) * g.ldo + col] = rmda_f2h(h);
+                    for (int v = 0; v < 4; v += 1) {
+                        const uint32_t rr = wm * 64 + i * 16 + rq + v;
+                        if (rr < c_rows) {
+#pragma unroll
+                            for (int j = 0; j < 4; j += 1) {
+                                const uint32_t col = c_nt * BN + wn * 64 + j * 16 + fr;
+                                O[(size_t)(c_row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
+                            }
+                        }
+                    }
+                }
+            } else {
+                // a 64-row group of B rows is 32 gate rows then the 32
+                // matching up rows: blocks j (gate) and j + 2 (up) hold the
+                // same output columns
+                const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
+                const uint32_t colbase = slab * 64 + (((wn * 64) % SLAB) / 64) * 32;
+#pragma unroll
+                for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                    for (int v = 0; v < 4; v += 1) {
+                        const uint32_t rr = wm * 64 + i * 16 + rq + v;
+                        if (rr < c_rows) {
+#pragma unroll
+                            for (int j = 0; j < 2; j += 1) {
+                                const float gt = acc[i][j][v];
+                                const float up = acc[i][j + 2][v];
+                                const float h = gt / (1.0f + __expf(-gt)) * up;
+                                O[(size_t)(c_row0 + rr) * g.ldo + colbase + j * 16 + fr] = rmda_f2h(h);
+                            }
                         }
                     }
                 }
             }
         }
+        ks += 1;
+        if (ks == steps) {
+            ks = 0;
+            kc += 1;
+        }
+    };
+    auto compute = [&](const frag_t &fa, const frag_t &fb) __attribute__((always_inline)) {
+        compute_begin();
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+                mfma_group(fa, fb, i);
+            }
+        }
+        compute_end();
+    };
+
+    // Iteration g: wait for stage g (later issued stages stay in flight),
+    // barrier, multiply stage g while issuing stage g + STAGES - 1 into the
+    // buffer stage g - 1 used (every wave passed this barrier after its reads
+    // of that buffer).
+    constexpr int LHI = (int)(A_PER + B_HI);
+    constexpr int LLO = (int)(A_PER + B_LO);
+#pragma unroll
+    for (uint32_t s = 0; s < STAGES - 1; s += 1) {
+        if (s < nstage) {
+            issue_next(s);
+        }
+    }
+    uint32_t ibuf = (STAGES - 1) % STAGES;  // buffer of the next stage to issue
+    uint32_t cbuf = 0;                      // buffer of the stage to multiply
+    uint32_t gs = 0;
+    // steady state: STAGES-2 later stages in flight and one to issue
+    const uint32_t steady = nstage > STAGES - 1 ? nstage - (STAGES - 1) : 0;
+#pragma nounroll
+    for (; gs < steady; gs += 1) {
+        if (b_hi) {
+            wait_vm<(STAGES - 2) * LHI>();
+        } else {
+            wait_vm<(STAGES - 2) * LLO>();
+        }
+        lds_barrier();
+        // MFMA groups and this wave's DMA instructions alternate: issuing
+        // DMA stalls while the CU's load path drains other waves' requests,
+        // and the stall then overlaps MFMAs already in the pipe
+        load_frags(cbuf, fa0, fb0);
+        cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
+        compute_begin();
+        issue_begin(ibuf);
+        ibuf = ibuf + 1 == STAGES ? 0 : ibuf + 1;
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            if (live) {
+                mfma_group(fa0, fb0, i);
+            }
+            if ((uint32_t)i < A_PER + B_HI) {
+                issue_one((uint32_t)i);
+            }
+        }
+        issue_end();
+        compute_end();
+    }
+    // drain: nothing left to issue
+#pragma nounroll
+    for (; gs < nstage; gs += 1) {
+        const uint32_t later = nstage - 1 - gs;
+        if (b_hi) {
+            wait_after<LHI>(later);
+        } else {
+            wait_after<LLO>(later);
+        }
+        lds_barrier();
+        load_frags(cbuf, fa0, fb0);
+        cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
+        compute(fa0, fb0);
     }
 }
 
@@ -361,59 +506,39 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t *__restrict__ 
 template <int MODE, int BN, int BK, int STAGES>
 hipError_t launch_cfg(hipStream_t s, const rmda_gemm_args_t *a, dim3 grid, bool packed) {
     if (packed) {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true>), grid, dim3(NT), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true>), grid, dim3(BM / 64 * BN), 0, s, *a);
     } else {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false>), grid, dim3(NT), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false>), grid, dim3(BM / 64 * BN), 0, s, *a);
     }
     return hipGetLastError();
 }
 
 template <int MODE>
 hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm2_cfg_t &c, bool packed) {
-    const uint32_t ntiles = a->n_w / SLAB / (c.bn / SLAB);
-    uint64_t blocks = (uint64_t)a->max_items * ntiles;
-    if (blocks == 0) {
+    if (a->max_items == 0) {
         return hipSuccess;
     }
-    blocks = (blocks + 7) / 8 * 8;
-    if (blocks > 0x7fffffffull) {
-        return hipErrorInvalidValue;
+    // persistent: one workgroup per CU, a multiple of the 8 XCDs
+    const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
+    const dim3 grid(wgs);
+    if (c.stages == 4) {
+        return launch_cfg<MODE, 256, 32, 4>(s, a, grid, packed);
     }
-    const dim3 grid((uint32_t)blocks);
-    if (c.bn == 256) {
-        if (c.bk == 64) {
-            return launch_cfg<MODE, 256, 64, 2>(s, a, grid, packed);
-        }
-        if (c.stages == 4) {
-            return launch_cfg<MODE, 256, 32, 4>(s, a, grid, packed);
-        }
+    if (c.stages == 3) {
         return launch_cfg<MODE, 256, 32, 3>(s, a, grid, packed);
     }
-    if (c.bk == 64) {
-        if (c.stages == 2) {
-            return launch_cfg<MODE, 128, 64, 2>(s, a, grid, packed);
-        }
-        return launch_cfg<MODE, 128, 64, 3>(s, a, grid, packed);
-    }
-    if (c.stages == 4) {
-        return launch_cfg<MODE, 128, 32, 4>(s, a, grid, packed);
-    }
-    return launch_cfg<MODE, 128, 32, 3>(s, a, grid, packed);
+    return launch_cfg<MODE, 256, 32, 5>(s, a, grid, packed);
 }
 
 }  // namespace
 
 // Variant 0 is the default: the fastest configuration measured on MI355X at
-// the benchmark shapes (BN 256, BK 64, two stages: 128 KiB of LDS).
+// the benchmark shapes.  LDS per workgroup = STAGES * (192 + BN) * BK * 2.
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     switch (variant) {
-    case 1: return {128, 32, 3};
-    case 2: return {128, 32, 4};
-    case 3: return {256, 32, 3};
-    case 4: return {256, 32, 4};
-    case 6: return {128, 64, 2};
-    case 7: return {128, 64, 3};
-    default: return {256, 64, 2};
+    case 1: return {256, 32, 4, 0};
+    case 2: return {256, 32, 3, 0};
+    default: return {256, 32, 5, 0};
     }
 }
 
@@ -422,7 +547,7 @@ hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm
         return hipErrorInvalidValue;
     }
     if ((a->n_w / SLAB) % (c.bn / SLAB) != 0) {
-        c.bn = 128;  // odd slab count: fall back to one slab per tile
+        return hipErrorInvalidValue;  // an N tile is two 128-row slabs
     }
     if (a->mode == RMDA_GEMM_SWIGLU) {
         return launch_mode<RMDA_GEMM_SWIGLU>(s, a, c, packed != 0);

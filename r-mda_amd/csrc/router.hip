@@ -7,18 +7,20 @@
 // a sequential fmaf chain over i = qL .. qL+L-1 starting from 0; the eight
 // partials are added left to right, then the bias.
 //
-// Work split: a workgroup owns a 32-token x 32-column output tile.  Its 256
-// threads are 8 chunk groups x 32 threads; each thread keeps 8 tokens x 4
-// columns of one chunk's partials in registers (32 independent fmaf chains)
-// and walks its chunk in steps of 16 through LDS, double-buffered.  The
-// eight partials then meet in LDS and are summed in chunk order.
-// Vector fp32 FMA (MFMA's internal summation order is not reproducible on a
-// CPU); the kernel is VALU-bound: rows*cols*d FMAs.
+// Work split: a workgroup owns a 16-token x 32-column output tile (512
+// workgroups at T=2048, E=128: two or three resident per CU, so global-load
+// latency hides behind other workgroups' FMAs).  Its 256 threads are 8 chunk
+// groups x 32 threads; each thread keeps 4 tokens x 4 columns of one chunk's
+// partials in registers (16 independent fmaf chains) and walks its chunk in
+// steps of 16 through LDS, double-buffered; within a wave the x reads are
+// 8-way broadcasts.  The eight partials then meet in LDS and are summed in
+// chunk order.  Vector fp32 FMA (MFMA's internal summation order is not
+// reproducible on a CPU).
 #include "common.h"
 
 namespace {
 
-constexpr int TM = 32;  // tokens per tile
+constexpr int TM = 16;  // tokens per tile
 constexpr int TC = 32;  // columns per tile
 constexpr int BK = 16;  // k per step inside a chunk
 constexpr int NQ = 8;   // chunks
@@ -52,44 +54,47 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     const uint32_t L = d / NQ;
     const uint32_t steps = L / BK;
 
-    // loader roles: (chunk lq, token/column lr)
+    // loader roles: x: (chunk, token, half of the 16-element step); w: (chunk, column)
     const uint32_t lq = tid / 32;
-    const uint32_t lr = tid % 32;
-    const bool xok = t0 + lr < rows;
-    const bool wok = c0 + lr < cols;
-    const uint16_t *xrow = x16 + (size_t)(xok ? t0 + lr : 0) * d + lq * L;
-    const float *wrow = w + (size_t)(wok ? c0 + lr : 0) * d + lq * L;
+    const uint32_t lx = (tid % 32) / 2;
+    const uint32_t lh = tid % 2;
+    const uint32_t lc = tid % 32;
+    const bool xok = t0 + lx < rows;
+    const bool wok = c0 + lc < cols;
+    const uint16_t *xrow = x16 + (size_t)(xok ? t0 + lx : 0) * d + lq * L + lh * 8;
+    const float *wrow = w + (size_t)(wok ? c0 + lc : 0) * d + lq * L;
 
-    // compute roles: (chunk q, 8 tokens tb*8.., 4 columns cb*4..)
+    // compute roles: (chunk q, 4 tokens tb*4.., 4 columns cb*4..)
     const uint32_t q = tid / 32;
     const uint32_t tb = (tid % 32) / 8;
     const uint32_t cb = tid % 8;
 
-    uint4 xr[2];
+    uint4 xr;
     float4 wr[4];
     auto gload = [&](uint32_t s) {
-        const uint4 *xp = reinterpret_cast<const uint4 *>(xrow + s * BK);
+        xr = xok ? *reinterpret_cast<const uint4 *>(xrow + s * BK) : make_uint4(0, 0, 0, 0);
         const float4 *wp = reinterpret_cast<const float4 *>(wrow + s * BK);
-        xr[0] = xok ? xp[0] : make_uint4(0, 0, 0, 0);
-        xr[1] = xok ? xp[1] : make_uint4(0, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i += 1) {
             wr[i] = wok ? wp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto lstore = [&](int buf) {
-        const uint16_t *xh = reinterpret_cast<const uint16_t *>(xr);
+        const uint16_t *xh = reinterpret_cast<const uint16_t *>(&xr);
         const float *wf = reinterpret_cast<const float *>(wr);
 #pragma unroll
+        for (int i = 0; i < 8; i += 1) {
+            sm.u.s.xs[buf][lq][lh * 8 + i][lx] = rmda_h2f(xh[i]);
+        }
+#pragma unroll
         for (int i = 0; i < BK; i += 1) {
-            sm.u.s.xs[buf][lq][i][lr] = rmda_h2f(xh[i]);
-            sm.u.s.ws[buf][lq][i][lr] = wf[i];
+            sm.u.s.ws[buf][lq][i][lc] = wf[i];
         }
     };
 
-    float acc[8][4];
+    float acc[4][4];
 #pragma unroll
-    for (int a = 0; a < 8; a += 1) {
+    for (int a = 0; a < 4; a += 1) {
 #pragma unroll
         for (int b = 0; b < 4; b += 1) {
             acc[a][b] = 0.0f;
@@ -104,15 +109,14 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
         if (s + 1 < steps) {
             gload(s + 1);
         }
-#pragma unroll 4
+#pragma unroll 8
         for (int i = 0; i < BK; i += 1) {
-            const float4 xa = *reinterpret_cast<const float4 *>(&sm.u.s.xs[buf][q][i][tb * 8]);
-            const float4 xb = *reinterpret_cast<const float4 *>(&sm.u.s.xs[buf][q][i][tb * 8 + 4]);
+            const float4 xa = *reinterpret_cast<const float4 *>(&sm.u.s.xs[buf][q][i][tb * 4]);
             const float4 wv = *reinterpret_cast<const float4 *>(&sm.u.s.ws[buf][q][i][cb * 4]);
-            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            const float xv[4] = {xa.x, xa.y, xa.z, xa.w};
             const float wf[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-            for (int a = 0; a < 8; a += 1) {
+            for (int a = 0; a < 4; a += 1) {
 #pragma unroll
                 for (int b = 0; b < 4; b += 1) {
                     acc[a][b] = __builtin_fmaf(xv[a], wf[b], acc[a][b]);
@@ -127,10 +131,10 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
 
     // chunk partials -> LDS, then sum in chunk order (the xs/ws buffers are dead)
 #pragma unroll
-    for (int a = 0; a < 8; a += 1) {
+    for (int a = 0; a < 4; a += 1) {
 #pragma unroll
         for (int b = 0; b < 4; b += 1) {
-            sm.u.red[q][tb * 8 + a][cb * 4 + b] = acc[a][b];
+            sm.u.red[q][tb * 4 + a][cb * 4 + b] = acc[a][b];
         }
     }
     __syncthreads();

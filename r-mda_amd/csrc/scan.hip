@@ -162,9 +162,12 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     }
     __threadfence();
 
-    // Each thread owns experts e0 = 2t and e0+1: column prefix of hist over
-    // blocks (other blocks' writes read at device scope), then padded widths,
-    // offsets, and per-block bases, all on entries this thread wrote itself.
+    // Each thread owns experts e0 = 2t and e0+1.  Pass 1: column totals of
+    // hist over blocks (other blocks' words read at device scope, RB loads in
+    // flight at a time instead of one dependent round trip per block).
+    // Padded widths and offsets follow from one block-wide scan.  Pass 2:
+    // hist[b][e] <- off[e] + sum_{b'<b} hist[b'][e], again RB loads at a time.
+    constexpr uint32_t RB = 16;
     const uint32_t e0 = 2 * tid;
     uint32_t c0 = 0;
     uint32_t c1 = 0;
@@ -172,11 +175,16 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         const uint32_t e = e0 + j;
         if (e < E) {
             uint32_t acc = 0;
-            for (uint32_t bb = 0; bb < nb; bb += 1) {
-                uint32_t *hp = &a.hist[(size_t)bb * E + e];
-                const uint32_t h = rmda_load_agent(hp);
-                *hp = acc;
-                acc += h;
+            for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+                uint32_t h[RB];
+#pragma unroll
+                for (uint32_t u = 0; u < RB; u += 1) {
+                    h[u] = bb0 + u < nb ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e]) : 0u;
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < RB; u += 1) {
+                    acc += h[u];
+                }
             }
             if (j == 0) {
                 c0 = acc;
@@ -205,8 +213,20 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             if (a.count != nullptr) {
                 a.count[e] = j == 0 ? c0 : c1;
             }
-            for (uint32_t bb = 0; bb < nb; bb += 1) {
-                a.hist[(size_t)bb * E + e] += o;
+            uint32_t acc = o;
+            for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+                uint32_t h[RB];
+#pragma unroll
+                for (uint32_t u = 0; u < RB; u += 1) {
+                    h[u] = bb0 + u < nb ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e]) : 0u;
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < RB; u += 1) {
+                    if (bb0 + u < nb) {
+                        a.hist[(size_t)(bb0 + u) * E + e] = acc;
+                    }
+                    acc += h[u];
+                }
             }
         }
     }
