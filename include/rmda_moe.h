@@ -309,7 +309,8 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
  * out[r] = sum_j wt[r,j] * FFN_{idx[r,j]}(x[r]) (+ sigmoid(g_r) * FFN_shared(x[r])).
  * Expert segments are packed without padding (tile 1); the permutation is
  * the stable order of rmda_moe_scatter.  Requires d % 256 == 0,
- * inter % 64 == 0, shared % 64 == 0, experts <= 512, topk <= 16. */
+ * inter % 128 == 0, shared == 0 or shared == inter, experts <= 512,
+ * topk <= 16. */
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
                    const rmda_moe_layer_args_t *args);
 

@@ -113,8 +113,8 @@ struct LayerPlan {
 };
 
 int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
-    if (s->d == 0 || s->d % 128 != 0) {
-        snprintf(why, n, "d=%u must be a positive multiple of 128", s->d);
+    if (s->d == 0 || s->d % 256 != 0) {
+        snprintf(why, n, "d=%u must be a positive multiple of 256", s->d);
         return 0;
     }
     if (s->experts == 0 || s->experts > RMDA_MAX_EXPERTS) {
@@ -125,8 +125,8 @@ int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
         snprintf(why, n, "topk=%u must be in 1..min(%u, experts)", s->topk, RMDA_MAX_TOPK);
         return 0;
     }
-    if (s->inter == 0 || s->inter % 64 != 0) {
-        snprintf(why, n, "inter=%u must be a positive multiple of 64", s->inter);
+    if (s->inter == 0 || s->inter % 128 != 0) {
+        snprintf(why, n, "inter=%u must be a positive multiple of 128", s->inter);
         return 0;
     }
     if (s->shared != 0 && s->shared != s->inter) {

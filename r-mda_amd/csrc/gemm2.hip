@@ -23,11 +23,11 @@
 //     instruction writes 64 consecutive 16-byte slots, so the swizzle is
 //     applied on the global side: each lane fetches the chunk that belongs
 //     at its slot.
-//   * Packed weights (rmda_moe_pack_weights) store every 128-row x BK slab
-//     in exactly its LDS image order, so each DMA instruction reads one
-//     contiguous KiB and a whole stage of B is one contiguous block (the
-//     HF [out][in] layout would read BK-wide pieces of 128 rows 4-8 KiB
-//     apart).
+//   * Packed weights (rmda_moe_pack_weights) store every 256-row x BK slab
+//     (one N tile's K step) in exactly its LDS image order, so each DMA
+//     instruction reads one contiguous KiB and a whole stage of B is one
+//     contiguous 16 KiB block (the HF [out][in] layout would read BK-wide
+//     pieces of 256 rows 4 KiB apart).
 //   * The grid is renumbered XCD-aware from the real work count read on the
 //     device: XCD x gets a contiguous range of (item, N tile) pairs, so the N
 //     tiles of one item (which share A rows) meet in one L2 and the 8 XCDs
@@ -41,7 +41,7 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr uint32_t BM = RMDA_GEMM2_BM;  // rows per work item (three 64-row blocks)
-constexpr uint32_t SLAB = 128;          // packed slab height (B rows)
+constexpr uint32_t SLAB = 256;          // packed slab height (B rows) = the N tile
 
 // chunk swizzle of row r (BK/8 chunks per row): chunk c of row r sits in
 // slot c ^ ((r >> 1) & (BK/8 - 1)).  Chosen by measurement on gfx950
@@ -55,14 +55,15 @@ __device__ __forceinline__ uint32_t swz(uint32_t r) {
 }
 
 // B row of a group's weight matrix that slab row n of slab `slab` holds.
-// SWIGLU slabs interleave 32 gate rows and the 32 matching up rows twice, so
-// one wave's accumulators hold gate and up of the same output columns.
+// A SWIGLU slab is SLAB/64 groups of 32 gate rows followed by the 32
+// matching up rows, so one wave's accumulators hold gate and up of the same
+// output columns.
 template <int MODE>
 __device__ __forceinline__ uint32_t slab_row(uint32_t slab, uint32_t n, uint32_t inter) {
     if (MODE == RMDA_GEMM_SWIGLU) {
         const uint32_t bw = n / 64;
         const uint32_t within = n % 64;
-        const uint32_t c = slab * 64 + bw * 32 + (within % 32);
+        const uint32_t c = slab * (SLAB / 2) + bw * 32 + (within % 32);
         return within < 32 ? c : inter + c;
     }
     return slab * SLAB + n;
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                 // matching up rows: blocks j (gate) and j + 2 (up) hold the
                 // same output columns
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
-                const uint32_t colbase = slab * 64 + (((wn * 64) % SLAB) / 64) * 32;
+                const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
 #pragma unroll
                 for (int i = 0; i < 4; i += 1) {
 #pragma unroll

@@ -95,9 +95,9 @@ def test_workspace_layout_for_every_config(L, cfg_id):
     assert total >= rows * (cfg["inter"] + cfg["d"]) * 2
 
 
-@pytest.mark.parametrize("bad", [dict(d=100), dict(d=0), dict(experts=0), dict(experts=513), dict(topk=0),
-                                 dict(topk=17), dict(experts=4, topk=5), dict(inter=96), dict(shared=64),
-                                 dict(rows=1 << 28)])
+@pytest.mark.parametrize("bad", [dict(d=100), dict(d=0), dict(d=384), dict(experts=0), dict(experts=513),
+                                 dict(topk=0), dict(topk=17), dict(experts=4, topk=5), dict(inter=96),
+                                 dict(inter=192), dict(shared=64), dict(rows=1 << 28)])
 def test_workspace_rejects_bad_shapes(L, bad):
     s = shape(**bad)
     assert L.rmda_moe_workspace_bytes(ctypes.byref(s)) == 0
