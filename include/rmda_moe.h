@@ -283,7 +283,8 @@ typedef struct rmda_moe_layer_args_t {
     void *workspace;            /* >= rmda_moe_workspace_bytes(shape) bytes */
     size_t workspace_bytes;
     const uint16_t *packed;     /* weights from rmda_moe_pack_weights, or NULL: then
-                                   the GEMMs read w_gate_up / w_down / w_sh_* */
+                                   the kernels read w_router / w_gate_up / w_down /
+                                   w_sh_* (the HF tensors above are ignored when set) */
 } rmda_moe_layer_args_t;
 
 /* Device views into the workspace after rmda_moe_layer (byte offsets), so a
@@ -318,23 +319,27 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
  * upload, src/qwen.c:376-394: qwen_bf16 converts the bf16 expert weights to
  * fp16 in place after each layer's upload) ---- */
 
-/* Bytes of one layer's packed expert weights: routed gate_up and down, then
- * the shared expert's gate_up and down when shape->shared > 0 (fp16, same
- * element count as the HF tensors).  0 when the shape is rejected. */
+/* Bytes of one layer's packed weights: routed gate_up and down, the shared
+ * expert's gate_up and down when shape->shared > 0 (fp16, same element
+ * count as the HF tensors), then the fp32 router matrix (experts [+1 shared
+ * gate] rows, padded to a multiple of 64).  0 when the shape is rejected. */
 size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape);
 
-/* Reorder the HF-layout expert weights (w_gate_up [E][2I][d], w_down
- * [E][d][I], and w_sh_gate_up [2I_s][d], w_sh_down [d][I_s] when shared > 0)
- * into the order the grouped GEMM streams them: each 128-row x K-step slab
- * becomes one contiguous block in exactly the layout the kernel keeps it in
- * LDS, so every weight load is a contiguous KiB.  With bf16 != 0 the inputs
- * are bf16 and are converted to fp16 (round to nearest even) on the way, in
- * place of qwen_bf16.  Enqueued on the context stream; `packed` must hold
- * rmda_moe_packed_bytes(shape) bytes and must not overlap the inputs.  A
- * packed buffer is valid for contexts of the same library build. */
-int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const uint16_t *w_gate_up,
-                          const uint16_t *w_down, const uint16_t *w_sh_gate_up, const uint16_t *w_sh_down,
-                          int bf16, uint16_t *packed);
+/* Reorder one layer's HF-layout weights (w_router [E (+1)][d] fp32,
+ * w_gate_up [E][2I][d], w_down [E][d][I], and w_sh_gate_up [2I_s][d],
+ * w_sh_down [d][I_s] when shared > 0) into the order the kernels stream
+ * them.  Each 256-row x K-step expert-weight slab becomes one contiguous
+ * block in exactly the layout the grouped GEMM keeps it in LDS, so every
+ * weight load is a contiguous KiB; the router matrix becomes [d/4][cols][4]
+ * so that one wave's router-weight load (64 columns x 4 k) is a contiguous
+ * KiB.  With bf16 != 0 the expert weights are bf16 and are converted to
+ * fp16 (round to nearest even) on the way, in place of qwen_bf16; the router
+ * matrix is copied exactly.  Enqueued on the context stream; `packed` must
+ * hold rmda_moe_packed_bytes(shape) bytes and must not overlap the inputs.
+ * A packed buffer is valid for contexts of the same library build. */
+int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const float *w_router,
+                          const uint16_t *w_gate_up, const uint16_t *w_down, const uint16_t *w_sh_gate_up,
+                          const uint16_t *w_sh_down, int bf16, uint16_t *packed);
 
 /* ---- stage profiler (replaces the reference's timestamp profiler:
  * mda_vkc_prof_begin / mda_vkc_prof_mark / mda_vkc_prof_report,

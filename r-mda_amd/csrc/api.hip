@@ -176,18 +176,22 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
 }
 
 // element offsets (halves) of the four weight sets inside a packed buffer
+// Offsets in 16-bit units.  Every region size is a multiple of 256 units
+// (d % 256 == 0), so each region starts 512-byte aligned.
 struct PackPlan {
-    size_t gate_up, down, sh_gate_up, sh_down, total;
+    size_t gate_up, down, sh_gate_up, sh_down, router, total;
 };
 
 PackPlan plan_pack(const rmda_moe_shape_t *s) {
     PackPlan p{};
     const size_t d = s->d;
+    const uint32_t cols = s->experts + (s->shared > 0 ? 1u : 0u);
     p.gate_up = 0;
     p.down = p.gate_up + (size_t)s->experts * 2 * s->inter * d;
     p.sh_gate_up = p.down + (size_t)s->experts * d * s->inter;
     p.sh_down = p.sh_gate_up + (size_t)2 * s->shared * d;
-    p.total = p.sh_down + d * s->shared;
+    p.router = p.sh_down + d * s->shared;
+    p.total = p.router + 2 * d * rmda_router_cpad(cols);  // fp32
     return p;
 }
 
@@ -589,7 +593,7 @@ int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint
     if (pc->rows == 0) {
         return RMDA_OK;
     }
-    return hip_check(ctx, rmda_launch_router(ctx->stream, x16, w, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
+    return hip_check(ctx, rmda_launch_router(ctx->stream, x16, w, 0, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
                                              bias != nullptr ? pc->nbias : 0, nullptr, 0),
                      "router");
 }
@@ -675,6 +679,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     const uint16_t *w_dn = packed != nullptr ? packed + pk.down : args->w_down;
     const uint16_t *w_sgu = packed != nullptr ? packed + pk.sh_gate_up : args->w_sh_gate_up;
     const uint16_t *w_sdn = packed != nullptr ? packed + pk.sh_down : args->w_sh_down;
+    const float *w_rt = packed != nullptr ? reinterpret_cast<const float *>(packed + pk.router) : args->w_router;
 
     if (ctx->prof_on && ctx->prof_pending == RMDA_PROF_RING) {
         rc = prof_harvest(ctx);
@@ -686,8 +691,8 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     // A0 router projection (+ zero the rank ticket for this call)
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
-                       rmda_launch_router(s, args->x, args->w_router, args->bias, proj, T, d, p.ps, p.ps,
-                                          args->bias != nullptr ? E : 0, done, 1),
+                       rmda_launch_router(s, args->x, w_rt, packed != nullptr, args->bias, proj, T, d, p.ps,
+                                          p.ps, args->bias != nullptr ? E : 0, done, 1),
                        "layer router");
     }
     if (rc == RMDA_OK) {
@@ -805,14 +810,14 @@ size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape) {
     return plan_pack(shape).total * 2;
 }
 
-int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const uint16_t *w_gate_up,
-                          const uint16_t *w_down, const uint16_t *w_sh_gate_up, const uint16_t *w_sh_down, int bf16,
-                          uint16_t *packed) {
+int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const float *w_router,
+                          const uint16_t *w_gate_up, const uint16_t *w_down, const uint16_t *w_sh_gate_up,
+                          const uint16_t *w_sh_down, int bf16, uint16_t *packed) {
     int rc = enter(ctx);
     if (rc != RMDA_OK) {
         return rc;
     }
-    if (shape == nullptr || w_gate_up == nullptr || w_down == nullptr || packed == nullptr ||
+    if (shape == nullptr || w_router == nullptr || w_gate_up == nullptr || w_down == nullptr || packed == nullptr ||
         (shape->shared > 0 && (w_sh_gate_up == nullptr || w_sh_down == nullptr))) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_pack_weights: null argument");
     }
@@ -836,6 +841,12 @@ int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
     if (rc == RMDA_OK && S > 0) {
         rc = hip_check(ctx, rmda_launch_pack(s, w_sh_down, packed + pk.sh_down, 1, d, S, S, 0, bk, bf16),
                        "pack shared down");
+    }
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx,
+                       rmda_launch_router_pack(s, w_router, reinterpret_cast<float *>(packed + pk.router),
+                                               E + (S > 0 ? 1u : 0u), d),
+                       "pack router");
     }
     return rc;
 }

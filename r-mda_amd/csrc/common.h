@@ -46,9 +46,12 @@ __device__ __forceinline__ float rmda_key_float(uint32_t k) {
 // hipGetLastError() after the launch.
 
 // router.hip
-hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, const float *bias,
+hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
                               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero);
+// Packed router weights: [d/4][rmda_router_cpad(cols)][4] fp32.
+uint32_t rmda_router_cpad(uint32_t cols);
+hipError_t rmda_launch_router_pack(hipStream_t s, const float *w, float *out, uint32_t cols, uint32_t d);
 
 // route.hip: top-k per row; count gets atomic adds (caller zeroes it first).
 hipError_t rmda_launch_route(hipStream_t s, const float *proj, uint32_t *idx, float *wt,

@@ -5,17 +5,32 @@
 // be bit-exact, so the logits follow one fixed order that the CPU oracle
 // replays: d is cut into 8 contiguous chunks of L = d/8; chunk q's partial is
 // a sequential fmaf chain over i = qL .. qL+L-1 starting from 0; the eight
-// partials are added left to right, then the bias.
+// partials are added left to right, then the bias.  Vector fp32 FMA (MFMA's
+// internal summation order is not reproducible on a CPU).
 //
-// Work split: a workgroup owns a 16-token x 32-column output tile (512
-// workgroups at T=2048, E=128: two or three resident per CU, so global-load
-// latency hides behind other workgroups' FMAs).  Its 256 threads are 8 chunk
-// groups x 32 threads; each thread keeps 4 tokens x 4 columns of one chunk's
-// partials in registers (16 independent fmaf chains) and walks its chunk in
-// steps of 16 through LDS, double-buffered; within a wave the x reads are
-// 8-way broadcasts.  The eight partials then meet in LDS and are summed in
-// chunk order.  Vector fp32 FMA (MFMA's internal summation order is not
-// reproducible on a CPU).
+// Two kernels compute the same bits:
+//
+// router_sx_kernel (d % 128 == 0; the layer always uses it).  A workgroup
+// owns 8 tokens x 64 columns; its 8 waves are the 8 d chunks.  Lane =
+// column: each lane streams its own column's weights while the 8 tokens'
+// fp16 activations are wave-uniform and arrive through scalar loads into
+// SGPRs, so every FMA is one v_fma_mix_f32 (fp16 SGPR operand widened
+// exactly, fp32 weight, fp32 accumulator, one rounding: the same value as
+// fmaf on the widened operand) and no LDS traffic or barrier sits in the k
+// loop.  With packed weights ([d/4][cols padded to 64][4], written once by
+// router_pack_kernel) one wave's weight load is 1 KiB contiguous; with HF
+// [cols][d] weights each lane reads its own row, which costs the L1 64
+// cache-line lookups per wave load and makes that variant about 40% slower.
+// Latency is hidden by 16 waves per CU rather than by in-wave prefetch:
+// scalar loads return out of order, so the compiler can only wait for all
+// of them, and a prefetched batch would be waited for with the current one.
+// The 8 chunk partials meet in LDS once at the end.
+//
+// router_tile_kernel (any d % 32 == 0; the standalone entry point uses it
+// when d % 128 != 0).  A workgroup owns 16 tokens x 32 columns; 256 threads
+// = 8 chunk groups x 32, each thread keeps 4 tokens x 4 columns of one
+// chunk's partials in registers and walks its chunk through a
+// double-buffered LDS tile.
 #include "common.h"
 
 namespace {
@@ -35,7 +50,7 @@ struct Smem {
     } u;
 };
 
-__global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict__ x16,
+__global__ __launch_bounds__(256) void router_tile_kernel(const uint16_t *__restrict__ x16,
                                                      const float *__restrict__ w,
                                                      const float *__restrict__ bias,
                                                      float *__restrict__ proj, uint32_t rows,
@@ -155,16 +170,151 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t *__restrict_
     }
 }
 
+
+constexpr int SX_BATCH = 8;  // k elements per scalar load (16 bytes per token)
+
+typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
+
+__device__ __forceinline__ float h_lo(uint32_t v) { return rmda_h2f((uint16_t)(v & 0xffffu)); }
+__device__ __forceinline__ float h_hi(uint32_t v) { return rmda_h2f((uint16_t)(v >> 16)); }
+
+// W_PACKED: w is the packed router layout [d/4][cpad][4] (see
+// router_pack_kernel), so lane c's four consecutive k values are 16 bytes
+// and one wave's load is 1 KiB contiguous.  Otherwise w is HF [cols][d] and
+// every lane reads its own row (64 cache lines per wave load).
+template <int RT, bool W_PACKED>
+__global__ __launch_bounds__(512) void router_sx_kernel(const uint16_t *__restrict__ x16,
+                                                        const float *__restrict__ w,
+                                                        const float *__restrict__ bias,
+                                                        float *__restrict__ proj, uint32_t rows, uint32_t d,
+                                                        uint32_t cols, uint32_t cpad, uint32_t stride,
+                                                        uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
+    __shared__ float red[NQ][RT][RMDA_WAVE];
+
+    const uint32_t lane = threadIdx.x % RMDA_WAVE;
+    const uint32_t q = __builtin_amdgcn_readfirstlane(threadIdx.x / RMDA_WAVE);
+    if (zero_words != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+        for (uint32_t i = threadIdx.x; i < n_zero; i += 512) {
+            zero_words[i] = 0;
+        }
+    }
+    const uint32_t L = d / NQ;
+    const uint32_t nb = L / SX_BATCH;  // even: d % 128 == 0 is a launch condition
+    const uint32_t t0 = blockIdx.x * RT;
+    const uint32_t c = blockIdx.y * RMDA_WAVE + lane;
+    const bool cok = c < cols;
+    const float4 *wp;
+    size_t wstep;  // float4s between consecutive 4-element groups of k
+    if (W_PACKED) {
+        wp = reinterpret_cast<const float4 *>(w) + (size_t)(q * L / 4) * cpad + c;
+        wstep = cpad;
+    } else {
+        wp = reinterpret_cast<const float4 *>(w + (size_t)(cok ? c : 0) * d + q * L);
+        wstep = 1;
+    }
+    // token rows past `rows` re-read the last row and are never stored
+    const_u32p xr[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t += 1) {
+        const uint32_t tok = t0 + t < rows ? t0 + t : rows - 1;
+        xr[t] = (const_u32p)(x16 + (size_t)tok * d + q * L);
+    }
+
+    float acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t += 1) {
+        acc[t] = 0.0f;
+    }
+#pragma unroll 2
+    for (uint32_t b = 0; b < nb; b += 1) {
+        const float4 w0 = wp[(size_t)(2 * b) * wstep];
+        const float4 w1 = wp[(size_t)(2 * b + 1) * wstep];
+        const float wf[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int t = 0; t < RT; t += 1) {
+            const const_u32p xp = xr[t] + b * 4;
+            const uint32_t xw[4] = {xp[0], xp[1], xp[2], xp[3]};
+#pragma unroll
+            for (int j = 0; j < 4; j += 1) {
+                acc[t] = __builtin_fmaf(h_lo(xw[j]), wf[2 * j], acc[t]);
+                acc[t] = __builtin_fmaf(h_hi(xw[j]), wf[2 * j + 1], acc[t]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int t = 0; t < RT; t += 1) {
+        red[q][t][lane] = acc[t];
+    }
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < RT * RMDA_WAVE; o += 512) {
+        const uint32_t t = o / RMDA_WAVE;
+        const uint32_t l = o % RMDA_WAVE;
+        const uint32_t cc = blockIdx.y * RMDA_WAVE + l;
+        float v = red[0][t][l];
+#pragma unroll
+        for (int qq = 1; qq < NQ; qq += 1) {
+            v = v + red[qq][t][l];
+        }
+        if (bias != nullptr && cc < nbias) {
+            v = v + bias[cc];
+        }
+        if (t0 + t < rows && cc < cols) {
+            proj[(size_t)(t0 + t) * stride + cc] = v;
+        }
+    }
+}
+
+// HF router weights [cols][d] -> packed [d/4][cpad][4], zero columns past
+// `cols`.  One thread per packed float; a one-time load-time reorder.
+__global__ __launch_bounds__(256) void router_pack_kernel(const float *__restrict__ w, float *__restrict__ out,
+                                                          uint32_t cols, uint32_t cpad, uint32_t d) {
+    const size_t n = (size_t)d * cpad;
+    for (size_t o = (size_t)blockIdx.x * 256 + threadIdx.x; o < n; o += (size_t)gridDim.x * 256) {
+        const uint32_t j = (uint32_t)(o % 4);
+        const uint32_t c = (uint32_t)((o / 4) % cpad);
+        const uint32_t i4 = (uint32_t)(o / (4 * (size_t)cpad));
+        out[o] = c < cols ? w[(size_t)c * d + i4 * 4 + j] : 0.0f;
+    }
+}
+
 }  // namespace
 
-hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, const float *bias,
+uint32_t rmda_router_cpad(uint32_t cols) { return (cols + RMDA_WAVE - 1) / RMDA_WAVE * RMDA_WAVE; }
+
+hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
                               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
+    constexpr int RT = 8;
+    static const int force_tile = getenv("RMDA_MOE_ROUTER_TILE") != nullptr;
+    if (w_packed && (d % 128 != 0 || rows == 0)) {
+        return hipErrorInvalidValue;
+    }
+    if (w_packed || (d % 128 == 0 && rows > 0 && !force_tile)) {
+        dim3 grid((rows + RT - 1) / RT, (cols + RMDA_WAVE - 1) / RMDA_WAVE);
+        const uint32_t cpad = rmda_router_cpad(cols);
+        if (w_packed) {
+            hipLaunchKernelGGL((router_sx_kernel<RT, true>), grid, dim3(512), 0, s, x16, w, bias, proj, rows, d,
+                               cols, cpad, stride, nbias, zero_words, n_zero);
+        } else {
+            hipLaunchKernelGGL((router_sx_kernel<RT, false>), grid, dim3(512), 0, s, x16, w, bias, proj, rows, d,
+                               cols, cpad, stride, nbias, zero_words, n_zero);
+        }
+        return hipGetLastError();
+    }
     dim3 grid((rows + TM - 1) / TM, (cols + TC - 1) / TC);
     if (rows == 0) {
         grid.x = 1;  // still run block (0,0) for the zero fill
     }
-    hipLaunchKernelGGL(router_kernel, grid, dim3(256), 0, s, x16, w, bias, proj, rows, d, cols, stride,
+    hipLaunchKernelGGL(router_tile_kernel, grid, dim3(256), 0, s, x16, w, bias, proj, rows, d, cols, stride,
                        nbias, zero_words, n_zero);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_router_pack(hipStream_t s, const float *w, float *out, uint32_t cols, uint32_t d) {
+    const uint32_t cpad = rmda_router_cpad(cols);
+    const size_t n = (size_t)d * cpad;
+    const uint32_t blocks = (uint32_t)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(router_pack_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, s, w, out, cols, cpad, d);
     return hipGetLastError();
 }

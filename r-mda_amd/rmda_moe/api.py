@@ -184,7 +184,8 @@ class Context:
                          workspace.numel() * workspace.element_size(), _ptr(packed))
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
 
-    def pack_weights(self, shape, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, bf16=False, packed=None):
+    def pack_weights(self, shape, w_router, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, bf16=False,
+                     packed=None):
         """rmda_moe_pack_weights into `packed` (allocated when None); returns it."""
         if packed is None:
             n = packed_bytes(shape)
@@ -192,9 +193,9 @@ class Context:
                 raise ValueError("shape rejected by rmda_moe_packed_bytes: %r" % (shape,))
             packed = torch.empty(n // 2, dtype=torch.float16, device=w_gate_up.device)
         s = shape_struct(shape)
-        self._check(self.L.rmda_moe_pack_weights(self.h, ctypes.byref(s), _ptr(w_gate_up), _ptr(w_down),
-                                                 _ptr(w_sh_gate_up), _ptr(w_sh_down), 1 if bf16 else 0,
-                                                 _ptr(packed)))
+        self._check(self.L.rmda_moe_pack_weights(self.h, ctypes.byref(s), _ptr(w_router), _ptr(w_gate_up),
+                                                 _ptr(w_down), _ptr(w_sh_gate_up), _ptr(w_sh_down),
+                                                 1 if bf16 else 0, _ptr(packed)))
         return packed
 
     # ---- stage profiler ----

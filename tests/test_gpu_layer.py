@@ -65,8 +65,11 @@ def check_layer(ctx, cfg, seed, n_sample=None):
     print("  max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
     # packed weights feed the MFMAs the same LDS images: bitwise the same output
-    packed = ctx.pack_weights(inp["shape"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"], inp["w_sh_down"])
-    out_p, _ = run_layer(ctx, inp, packed=packed)
+    proj = views["proj"].clone()
+    packed = ctx.pack_weights(inp["shape"], inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+    out_p, views_p = run_layer(ctx, inp, packed=packed)
+    assert torch.equal(views_p["proj"].view(torch.int32), proj.view(torch.int32)), "packed-router logits differ"
     assert torch.equal(out_p.view(torch.int16), out.view(torch.int16)), "packed-weight output differs"
     return out
 
@@ -113,16 +116,25 @@ def test_pack_bf16_input_equals_fp16_of_converted(ctx):
     g = torch.Generator(device="cuda").manual_seed(3)
     gu = (torch.randn(E, 2 * I, d, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
     dn = (torch.randn(E, d, I, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
-    p_bf = ctx.pack_weights(shape, gu.view(torch.float16), dn.view(torch.float16), bf16=True)
+    wr = torch.randn(E, d, device="cuda", generator=g, dtype=torch.float32)
+    p_bf = ctx.pack_weights(shape, wr, gu.view(torch.float16), dn.view(torch.float16), bf16=True)
     # reference conversion through the oracle's qwen_bf16 restatement
     gu16 = orc.qwen_bf16(gu.view(torch.int32).cpu().numpy().view(np.uint32))
     dn16 = orc.qwen_bf16(dn.view(torch.int32).cpu().numpy().view(np.uint32))
     gu_h = torch.from_numpy(gu16.view(np.int16)).cuda().view(torch.float16).view(E, 2 * I, d)
     dn_h = torch.from_numpy(dn16.view(np.int16)).cuda().view(torch.float16).view(E, d, I)
-    p_h = ctx.pack_weights(shape, gu_h, dn_h)
+    p_h = ctx.pack_weights(shape, wr, gu_h, dn_h)
     ctx.sync()
     assert torch.equal(p_bf.view(torch.int16), p_h.view(torch.int16))
-    # packing is a permutation of the elements
-    a = np.sort(p_h.view(torch.int16).cpu().numpy().ravel())
+    # expert-weight packing is a permutation of the elements
+    n_exp = E * 2 * I * d + E * d * I
+    a = np.sort(p_h.view(torch.int16).cpu().numpy()[:n_exp])
     b = np.sort(np.concatenate([gu16.view(np.int16).ravel(), dn16.view(np.int16).ravel()]))
     assert np.array_equal(a, b)
+    # the router matrix follows as [d/4][cols rounded up to 64][4] fp32, zero padded, bits unchanged
+    cpad = (E + 63) // 64 * 64
+    rt = p_h[n_exp:].view(torch.float32).cpu().numpy()
+    assert rt.size == d * cpad
+    want = np.zeros((d // 4, cpad, 4), np.float32)
+    want[:, :E, :] = wr.cpu().numpy().reshape(E, d // 4, 4).transpose(1, 0, 2)
+    assert np.array_equal(rt.view(np.uint32), want.reshape(-1).view(np.uint32))

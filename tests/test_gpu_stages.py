@@ -50,6 +50,9 @@ def test_fill_matches_oracle_bitwise(ctx, n, stream, seed, std):
     (2048, 2048, 128, 130, True),   # config 4 (skew bias), padded stride
     (512, 2048, 513, 513, False),   # config 5 row subset: 512 experts + shared gate
     (37, 256, 70, 72, True),        # ragged tile edges
+    (37, 2048, 70, 72, True),       # d = 2048 kernel: shifted last token tile, partial column group
+    (23, 2048, 513, 513, True),     # d = 2048 kernel, one column in the last group
+    (5, 2048, 128, 128, False),     # fewer rows than one token tile
 ])
 def test_router_bitexact(ctx, rows, d, cols, stride, bias):
     x = orc.fill_normal_f16(rows * d, configs.STREAM_X, 1, 1.0).reshape(rows, d)
