@@ -46,6 +46,7 @@ def parse_args():
     ap.add_argument("--cpu-tokens", type=int, default=None,
                     help="tokens in the CPU-baseline sample (default: sized for ~10-30 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true", help="skip re-measuring the copy and GEMM peaks")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a device copy of known size (HBM counter calibration)")
     ap.add_argument("--stages", action="store_true", help="print the stage table to stderr")
@@ -117,6 +118,44 @@ def cpu_baseline(inp, cfg, n_tokens, min_seconds=10.0, max_reps=4):
     }
 
 
+def measure_peaks(torch):
+    """This box's achievable peaks, re-measured as the reference measures
+    them: a device copy timed as 2*bytes/t (src/probe_memory.c:41-63,86) and
+    a large dense fp16 GEMM (rocBLAS/hipBLASLt through torch.matmul)."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * n / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e9
+    del src, dst
+    m = 8192
+    a = torch.randn(m, m, dtype=torch.float16, device="cuda")
+    b = torch.randn(m, m, dtype=torch.float16, device="cuda")
+    for _ in range(2):
+        c = a @ b
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        c = a @ b
+    e1.record()
+    torch.cuda.synchronize()
+    tf = 2.0 * m ** 3 / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.empty_cache()
+    return {"hbm_copy_GB/s": round(copy_gbs, 1), "hbm_copy": "1 GiB device copy, 2*bytes/t",
+            "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -163,18 +202,24 @@ def main():
     ctx.sync()
     torch.cuda.synchronize()
 
-    # timed region: K layer calls, bracketed by device synchronisation
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+    # timed region: K layer calls, bracketed by device synchronisation; events
+    # between equal rounds of the K calls (no synchronisation inside) give the
+    # best and median round, the reference's bench discipline
+    # (src/bench.c:32-53,93-105)
+    n_rounds = max(1, min(7, args.steps))
+    cuts = [args.steps * r // n_rounds for r in range(n_rounds + 1)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_rounds + 1)]
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
+    evs[0].record()
+    for r in range(n_rounds):
+        for _ in range(cuts[r + 1] - cuts[r]):
+            step()
+        evs[r + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    round_ms = sorted(evs[r].elapsed_time(evs[r + 1]) / (cuts[r + 1] - cuts[r]) for r in range(n_rounds))
 
     # per-stage durations: the same K calls again with the stage profiler on
     ctx.prof_begin()
@@ -241,6 +286,8 @@ def main():
         torch.cuda.synchronize()
         print("calib copy: %d bytes read, %d bytes written per launch" % (n, n), file=sys.stderr)
 
+    peaks = None if args.no_peaks else measure_peaks(torch)
+
     cpu = None
     if not args.no_cpu_baseline:
         n_tok = args.cpu_tokens
@@ -272,6 +319,8 @@ def main():
                    "tokens": T, "d": shape["d"], "experts": shape["experts"], "topk": shape["topk"],
                    "inter": shape["inter"], "shared": shape["shared"], "parallelism": "single GPU"},
         "wall_ms_per_step": round(1000.0 * wall / args.steps, 5),
+        "rounds": {"n": n_rounds, "best_ms": round(round_ms[0], 5),
+                   "median_ms": round(round_ms[len(round_ms) // 2], 5)},
         "weights": "HF layout" if args.hf_layout else "packed once before timing (%.1f ms, host-timed)" % pack_ms,
         "roofline": roof,
         "gemm": gemm,
@@ -281,6 +330,10 @@ def main():
     }
     if cpu is not None:
         line["cpu_baseline"]["gpu_over_cpu"] = round(line["value"] / cpu["value"], 1)
+    if peaks is not None:
+        line["peaks_measured"] = peaks
+        if roof["unit"] == "GB/s":
+            roof["frac_of_measured_copy"] = round(roof["achieved"] / peaks["hbm_copy_GB/s"], 4)
     ctx.close()
     print(json.dumps(line), flush=True)
 

@@ -594,7 +594,7 @@ int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint
         return RMDA_OK;
     }
     return hip_check(ctx, rmda_launch_router(ctx->stream, x16, w, 0, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
-                                             bias != nullptr ? pc->nbias : 0, nullptr, 0),
+                                             bias != nullptr ? pc->nbias : 0, nullptr, 0, nullptr),
                      "router");
 }
 
@@ -688,18 +688,22 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         }
     }
     rc = prof_mark(ctx, 0);
-    // A0 router projection (+ zero the rank ticket for this call)
+    // A0 router projection (+ zero the rank ticket for this call) with the A1
+    // top-k fused in when one workgroup can hold a token's whole logit row
+    const bool fuse_route = p.ps <= rmda_route_fuse_max_cols();
+    rmda_route_fuse_t fz{E, K, idx, wt};
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
                        rmda_launch_router(s, args->x, w_rt, packed != nullptr, args->bias, proj, T, d, p.ps,
-                                          p.ps, args->bias != nullptr ? E : 0, done, 1),
+                                          p.ps, args->bias != nullptr ? E : 0, done, 1,
+                                          fuse_route ? &fz : nullptr),
                        "layer router");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_ROUTER + 1);
     }
-    // A1 top-k
-    if (rc == RMDA_OK) {
+    // A1 top-k (unless fused above)
+    if (rc == RMDA_OK && !fuse_route) {
         rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
     }
     if (rc == RMDA_OK) {

@@ -41,6 +41,103 @@ __device__ __forceinline__ float rmda_key_float(uint32_t k) {
     return __builtin_bit_cast(float, u);
 }
 
+__device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        uint32_t lo = __shfl_xor((uint32_t)v, m);
+        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+        uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Top-k of one row of logits by one wave (shader/moe_route.comp:20-61):
+// topk rounds, each taking the largest untaken logit by strict '>' from
+// -3.0e38, so the lowest column wins ties and NaN / values <= -3e38 are never
+// taken; idx in selection order; z = sum_k exp(l_k - l_0) summed in
+// selection order; wt_k = exp(l_k - l_0) / z; count[e] += 1 per selection
+// when count != NULL.  Lane l holds columns l, l+64, ...; a round is one
+// lane-local scan plus one wave-wide max over the 64-bit key
+// (order-preserving float bits << 32 | ~column).  AGENT: read the logits
+// with device-scope loads (rows written by other workgroups of the running
+// kernel).
+template <int NV, bool AGENT>
+__device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts, uint32_t topk,
+                                               uint32_t *idx_row, float *wt_row, uint32_t *count) {
+    const uint32_t lane = threadIdx.x % RMDA_WAVE;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j += 1) {
+        const uint32_t c = lane + RMDA_WAVE * j;
+        if (c < experts) {
+            v[j] = AGENT ? __builtin_bit_cast(float, rmda_load_agent(reinterpret_cast<const uint32_t *>(l) + c))
+                         : l[c];
+        } else {
+            v[j] = -3.0e38f;  // -3e38 is never selectable
+        }
+    }
+    uint32_t taken = 0;
+    // z and the per-lane output are built round by round (lane k keeps round
+    // k's selection); z still accumulates in selection order
+    float sv0 = 0.0f;
+    float z = 0.0f;
+    uint32_t my_sel = RMDA_NONE;
+    float my_val = 0.0f;
+    for (uint32_t k = 0; k < topk; k += 1) {
+        float lb = -3.0e38f;
+        int lv = -1;
+#pragma unroll
+        for (int j = 0; j < NV; j += 1) {
+            if (((taken >> j) & 1u) == 0 && v[j] > lb) {
+                lb = v[j];
+                lv = j;
+            }
+        }
+        uint64_t key = 0;
+        if (lv >= 0) {
+            key = ((uint64_t)rmda_float_key(lb) << 32) | (uint32_t)(~(lane + RMDA_WAVE * (uint32_t)lv));
+        }
+        key = rmda_wave_max_u64(key);
+        uint32_t col = RMDA_NONE;
+        float val = -3.0e38f;
+        if (key != 0) {
+            col = ~(uint32_t)key;
+            val = rmda_key_float((uint32_t)(key >> 32));
+            if (col % RMDA_WAVE == lane) {
+                taken |= 1u << (col / RMDA_WAVE);
+            }
+        }
+        if (k == 0) {
+            sv0 = val;
+        }
+        z = z + expf(val - sv0);
+        if (lane == k) {
+            my_sel = col;
+            my_val = val;
+        }
+    }
+    if (lane < topk) {
+        idx_row[lane] = my_sel;
+        wt_row[lane] = expf(my_val - sv0) / z;
+        if (count != nullptr && my_sel != RMDA_NONE) {
+            atomicAdd(&count[my_sel], 1u);
+        }
+    }
+}
+
+// Router kernel with the top-k fused in: one workgroup owns all logits of
+// RMDA_ROUTE_GROUP tokens (cols <= rmda_route_fuse_max_cols()) and routes
+// them from LDS.
+struct rmda_route_fuse_t {
+    uint32_t experts;
+    uint32_t topk;
+    uint32_t *idx;       // [rows][topk]
+    float *wt;           // [rows][topk]
+};
+#define RMDA_ROUTE_GROUP 8u
+uint32_t rmda_route_fuse_max_cols();
+
 // ---- launch helpers implemented by the kernel files ----
 // Every launcher validates nothing: api.hip checks shapes first.  They return
 // hipGetLastError() after the launch.
@@ -48,7 +145,8 @@ __device__ __forceinline__ float rmda_key_float(uint32_t k) {
 // router.hip
 hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
-                              uint32_t nbias, uint32_t *zero_words, uint32_t n_zero);
+                              uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
+                              const rmda_route_fuse_t *fuse);
 // Packed router weights: [d/4][rmda_router_cpad(cols)][4] fp32.
 uint32_t rmda_router_cpad(uint32_t cols);
 hipError_t rmda_launch_router_pack(hipStream_t s, const float *w, float *out, uint32_t cols, uint32_t d);

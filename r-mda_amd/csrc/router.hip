@@ -182,26 +182,41 @@ __device__ __forceinline__ float h_hi(uint32_t v) { return rmda_h2f((uint16_t)(v
 // router_pack_kernel), so lane c's four consecutive k values are 16 bytes
 // and one wave's load is 1 KiB contiguous.  Otherwise w is HF [cols][d] and
 // every lane reads its own row (64 cache lines per wave load).
-template <int RT, bool W_PACKED>
-__global__ __launch_bounds__(512) void router_sx_kernel(const uint16_t *__restrict__ x16,
-                                                        const float *__restrict__ w,
-                                                        const float *__restrict__ bias,
-                                                        float *__restrict__ proj, uint32_t rows, uint32_t d,
-                                                        uint32_t cols, uint32_t cpad, uint32_t stride,
-                                                        uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
-    __shared__ float red[NQ][RT][RMDA_WAVE];
+//
+// CG column groups of 64 per workgroup (blockDim = 512 * CG; wave q works on
+// chunk q % 8 of column group q / 8).  FUSE (top-k fused in; CG * 64 >= cols,
+// one column slice): the workgroup owns every logit of its RT tokens, keeps
+// them in LDS, and its first RT waves route one token each, so the routing
+// needs no second launch and no hand-off between workgroups (which on this
+// multi-XCD part would need a device-scope fence, i.e. an L2 write-back).
+template <int RT, bool W_PACKED, int CG, bool FUSE>
+__global__ __launch_bounds__(512 * CG) void router_sx_kernel(const uint16_t *__restrict__ x16,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ bias,
+                                                             float *__restrict__ proj, uint32_t rows,
+                                                             uint32_t d, uint32_t cols, uint32_t cpad,
+                                                             uint32_t stride, uint32_t nbias,
+                                                             uint32_t *zero_words, uint32_t n_zero,
+                                                             rmda_route_fuse_t fz) {
+    constexpr uint32_t NT = 512 * CG;
+    constexpr uint32_t NCOL = RMDA_WAVE * CG;
+    __shared__ float red[NQ][RT][NCOL];
+    __shared__ float lg[RT][NCOL];
 
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
-    const uint32_t q = __builtin_amdgcn_readfirstlane(threadIdx.x / RMDA_WAVE);
+    const uint32_t wq = __builtin_amdgcn_readfirstlane(threadIdx.x / RMDA_WAVE);
+    const uint32_t q = wq % NQ;   // d chunk
+    const uint32_t cg = wq / NQ;  // column group within the workgroup
     if (zero_words != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
-        for (uint32_t i = threadIdx.x; i < n_zero; i += 512) {
+        for (uint32_t i = threadIdx.x; i < n_zero; i += NT) {
             zero_words[i] = 0;
         }
     }
     const uint32_t L = d / NQ;
     const uint32_t nb = L / SX_BATCH;  // even: d % 128 == 0 is a launch condition
     const uint32_t t0 = blockIdx.x * RT;
-    const uint32_t c = blockIdx.y * RMDA_WAVE + lane;
+    const uint32_t c0 = blockIdx.y * NCOL;
+    const uint32_t c = c0 + cg * RMDA_WAVE + lane;
     const bool cok = c < cols;
     const float4 *wp;
     size_t wstep;  // float4s between consecutive 4-element groups of k
@@ -225,7 +240,10 @@ __global__ __launch_bounds__(512) void router_sx_kernel(const uint16_t *__restri
     for (int t = 0; t < RT; t += 1) {
         acc[t] = 0.0f;
     }
-#pragma unroll 2
+    // two K batches per iteration where the SGPR budget allows it (the fused
+    // top-k tail's live values leave room for one)
+    constexpr int UNROLL = FUSE ? 1 : 2;
+#pragma unroll UNROLL
     for (uint32_t b = 0; b < nb; b += 1) {
         const float4 w0 = wp[(size_t)(2 * b) * wstep];
         const float4 w1 = wp[(size_t)(2 * b + 1) * wstep];
@@ -244,13 +262,13 @@ __global__ __launch_bounds__(512) void router_sx_kernel(const uint16_t *__restri
 
 #pragma unroll
     for (int t = 0; t < RT; t += 1) {
-        red[q][t][lane] = acc[t];
+        red[q][t][cg * RMDA_WAVE + lane] = acc[t];
     }
     __syncthreads();
-    for (uint32_t o = threadIdx.x; o < RT * RMDA_WAVE; o += 512) {
-        const uint32_t t = o / RMDA_WAVE;
-        const uint32_t l = o % RMDA_WAVE;
-        const uint32_t cc = blockIdx.y * RMDA_WAVE + l;
+    for (uint32_t o = threadIdx.x; o < RT * NCOL; o += NT) {
+        const uint32_t t = o / NCOL;
+        const uint32_t l = o % NCOL;
+        const uint32_t cc = c0 + l;
         float v = red[0][t][l];
 #pragma unroll
         for (int qq = 1; qq < NQ; qq += 1) {
@@ -259,9 +277,21 @@ __global__ __launch_bounds__(512) void router_sx_kernel(const uint16_t *__restri
         if (bias != nullptr && cc < nbias) {
             v = v + bias[cc];
         }
+        lg[t][l] = v;
         if (t0 + t < rows && cc < cols) {
             proj[(size_t)(t0 + t) * stride + cc] = v;
         }
+    }
+    if (!FUSE) {
+        return;
+    }
+    // fused top-k (fz.experts <= NCOL): wave t routes token t0 + t from LDS
+    __syncthreads();
+    const uint32_t t = t0 + wq;
+    if (wq < (uint32_t)RT && t < rows) {
+        uint32_t *ir = fz.idx + (size_t)t * fz.topk;
+        float *wr = fz.wt + (size_t)t * fz.topk;
+        rmda_route_row<CG, false>(&lg[wq][0], fz.experts, fz.topk, ir, wr, nullptr);
     }
 }
 
@@ -282,23 +312,48 @@ __global__ __launch_bounds__(256) void router_pack_kernel(const float *__restric
 
 uint32_t rmda_router_cpad(uint32_t cols) { return (cols + RMDA_WAVE - 1) / RMDA_WAVE * RMDA_WAVE; }
 
+template <int CG, bool FUSE>
+void launch_sx(hipStream_t s, dim3 grid, bool w_packed, const uint16_t *x16, const float *w, const float *bias,
+               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t cpad, uint32_t stride,
+               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
+    constexpr int RT = RMDA_ROUTE_GROUP;
+    if (w_packed) {
+        hipLaunchKernelGGL((router_sx_kernel<RT, true, CG, FUSE>), grid, dim3(512 * CG), 0, s, x16, w, bias, proj, rows,
+                           d, cols, cpad, stride, nbias, zero_words, n_zero, fz);
+    } else {
+        hipLaunchKernelGGL((router_sx_kernel<RT, false, CG, FUSE>), grid, dim3(512 * CG), 0, s, x16, w, bias, proj, rows,
+                           d, cols, cpad, stride, nbias, zero_words, n_zero, fz);
+    }
+}
+
 hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
-                              uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
-    constexpr int RT = 8;
-    static const int force_tile = getenv("RMDA_MOE_ROUTER_TILE") != nullptr;
-    if (w_packed && (d % 128 != 0 || rows == 0)) {
+                              uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
+                              const rmda_route_fuse_t *fuse) {
+    constexpr uint32_t RT = RMDA_ROUTE_GROUP;
+    const bool sx = d % 128 == 0 && rows > 0;
+    if ((w_packed || fuse != nullptr) && !sx) {
         return hipErrorInvalidValue;
     }
-    if (w_packed || (d % 128 == 0 && rows > 0 && !force_tile)) {
-        dim3 grid((rows + RT - 1) / RT, (cols + RMDA_WAVE - 1) / RMDA_WAVE);
+    if (fuse != nullptr && (fuse->experts > cols || cols > rmda_route_fuse_max_cols())) {
+        return hipErrorInvalidValue;
+    }
+    if (sx) {
         const uint32_t cpad = rmda_router_cpad(cols);
-        if (w_packed) {
-            hipLaunchKernelGGL((router_sx_kernel<RT, true>), grid, dim3(512), 0, s, x16, w, bias, proj, rows, d,
-                               cols, cpad, stride, nbias, zero_words, n_zero);
+        rmda_route_fuse_t fz{};
+        if (fuse != nullptr) {
+            fz = *fuse;
+        }
+        const uint32_t gx = (rows + RT - 1) / RT;
+        if (fuse != nullptr && cols > RMDA_WAVE) {
+            launch_sx<2, true>(s, dim3(gx, 1), w_packed, x16, w, bias, proj, rows, d, cols, cpad, stride, nbias,
+                               zero_words, n_zero, fz);
+        } else if (fuse != nullptr) {
+            launch_sx<1, true>(s, dim3(gx, 1), w_packed, x16, w, bias, proj, rows, d, cols, cpad, stride, nbias,
+                               zero_words, n_zero, fz);
         } else {
-            hipLaunchKernelGGL((router_sx_kernel<RT, false>), grid, dim3(512), 0, s, x16, w, bias, proj, rows, d,
-                               cols, cpad, stride, nbias, zero_words, n_zero);
+            launch_sx<1, false>(s, dim3(gx, (cols + RMDA_WAVE - 1) / RMDA_WAVE), w_packed, x16, w, bias, proj, rows,
+                                d, cols, cpad, stride, nbias, zero_words, n_zero, fz);
         }
         return hipGetLastError();
     }
@@ -310,6 +365,8 @@ hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w
                        nbias, zero_words, n_zero);
     return hipGetLastError();
 }
+
+uint32_t rmda_route_fuse_max_cols() { return 2 * RMDA_WAVE; }
 
 hipError_t rmda_launch_router_pack(hipStream_t s, const float *w, float *out, uint32_t cols, uint32_t d) {
     const uint32_t cpad = rmda_router_cpad(cols);

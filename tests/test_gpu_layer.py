@@ -91,6 +91,18 @@ def test_layer_other_seed_and_ragged(ctx):
     check_layer(ctx, cfg, seed=1)
 
 
+def test_layer_zero_rows_is_a_no_op(ctx):
+    """rows = 0 (an empty chunk) enqueues nothing harmful and returns OK."""
+    cfg = dict(configs.CONFIGS[3], rows=0, name="empty")
+    inp = inputs.make_inputs(ctx, dict(configs.CONFIGS[3], rows=8), seed=0)
+    shape = configs.shape_of(cfg)
+    ws = inputs.workspace_for(shape)
+    out = torch.full((1, shape["d"]), 3.0, dtype=torch.float16, device="cuda")  # pointers stay non-null
+    ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"], None, None, out, ws)
+    ctx.sync()
+    assert bool((out == 3.0).all()), "nothing may be written for rows = 0"
+
+
 def test_layer_deterministic(ctx):
     cfg = configs.CONFIGS[4]
     inp = inputs.make_inputs(ctx, cfg, seed=2)
