@@ -40,8 +40,8 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "gate_up_prefill_traffic.txt")
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=140)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=3, help="BASELINE configuration (1-5)")
     ap.add_argument("--cpu-tokens", type=int, default=None,
                     help="tokens in the CPU-baseline sample (default: sized for ~10-30 s)")
@@ -219,7 +219,8 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     ms = evs[0].elapsed_time(evs[-1]) / args.steps
-    round_ms = sorted(evs[r].elapsed_time(evs[r + 1]) / (cuts[r + 1] - cuts[r]) for r in range(n_rounds))
+    round_seq = [evs[r].elapsed_time(evs[r + 1]) / (cuts[r + 1] - cuts[r]) for r in range(n_rounds)]
+    round_ms = sorted(round_seq)
 
     # per-stage durations: the same K calls again with the stage profiler on
     ctx.prof_begin()
@@ -320,7 +321,8 @@ def main():
                    "inter": shape["inter"], "shared": shape["shared"], "parallelism": "single GPU"},
         "wall_ms_per_step": round(1000.0 * wall / args.steps, 5),
         "rounds": {"n": n_rounds, "best_ms": round(round_ms[0], 5),
-                   "median_ms": round(round_ms[len(round_ms) // 2], 5)},
+                   "median_ms": round(round_ms[len(round_ms) // 2], 5),
+                   "ms_in_order": [round(x, 4) for x in round_seq]},
         "weights": "HF layout" if args.hf_layout else "packed once before timing (%.1f ms, host-timed)" % pack_ms,
         "roofline": roof,
         "gemm": gemm,
