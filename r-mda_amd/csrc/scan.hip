@@ -145,12 +145,15 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         }
         __syncthreads();
     }
+    // Hand-off: the last block to arrive finalises.  The block totals are
+    // stored and later read with device-scope atomics, and each store has
+    // completed (vmcnt(0)) before the block takes its ticket, so the last
+    // block sees every total without a device-scope fence: on this multi-XCD
+    // part such a fence writes back and invalidates the whole L2.
     for (uint32_t e = tid; e < E; e += NT) {
-        a.hist[(size_t)b * E + e] = run[e];
+        __hip_atomic_store(&a.hist[(size_t)b * E + e], run[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-
-    // hand-off: the last block to arrive finalises
-    __threadfence();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
         // atomicInc wraps the ticket back to 0 on the last block
@@ -160,37 +163,34 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     if (!s_last) {
         return;
     }
-    __threadfence();
 
     // Each thread owns experts e0 = 2t and e0+1.  Pass 1: column totals of
-    // hist over blocks (other blocks' words read at device scope, RB loads in
-    // flight at a time instead of one dependent round trip per block).
-    // Padded widths and offsets follow from one block-wide scan.  Pass 2:
-    // hist[b][e] <- off[e] + sum_{b'<b} hist[b'][e], again RB loads at a time.
+    // hist over blocks (other blocks' words read at device scope, RB blocks
+    // of both experts in flight at a time instead of one dependent round trip
+    // per block).  Padded widths and offsets follow from one block-wide scan.
+    // Pass 2: hist[b][e] <- off[e] + sum_{b'<b} hist[b'][e], from the values
+    // pass 1 kept when nb <= RB, else reloaded RB blocks at a time.
     constexpr uint32_t RB = 16;
     const uint32_t e0 = 2 * tid;
+    const bool own0 = e0 < E;
+    const bool own1 = e0 + 1 < E;
+    uint32_t h0[RB], h1[RB];
+    auto load_batch = [&](uint32_t bb0) {
+#pragma unroll
+        for (uint32_t u = 0; u < RB; u += 1) {
+            const bool in = bb0 + u < nb;
+            h0[u] = in && own0 ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e0]) : 0u;
+            h1[u] = in && own1 ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e0 + 1]) : 0u;
+        }
+    };
     uint32_t c0 = 0;
     uint32_t c1 = 0;
-    for (uint32_t j = 0; j < 2; j += 1) {
-        const uint32_t e = e0 + j;
-        if (e < E) {
-            uint32_t acc = 0;
-            for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
-                uint32_t h[RB];
+    for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+        load_batch(bb0);
 #pragma unroll
-                for (uint32_t u = 0; u < RB; u += 1) {
-                    h[u] = bb0 + u < nb ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e]) : 0u;
-                }
-#pragma unroll
-                for (uint32_t u = 0; u < RB; u += 1) {
-                    acc += h[u];
-                }
-            }
-            if (j == 0) {
-                c0 = acc;
-            } else {
-                c1 = acc;
-            }
+        for (uint32_t u = 0; u < RB; u += 1) {
+            c0 += h0[u];
+            c1 += h1[u];
         }
     }
     const uint32_t p0 = (c0 + a.tile - 1u) / a.tile * a.tile;
@@ -200,34 +200,43 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     uint32_t o0 = base;
     uint32_t o1 = base + p0;
     if (a.off_in != nullptr) {
-        o0 = e0 < E ? a.off_in[e0] : 0u;
-        o1 = e0 + 1 < E ? a.off_in[e0 + 1] : 0u;
+        o0 = own0 ? a.off_in[e0] : 0u;
+        o1 = own1 ? a.off_in[e0 + 1] : 0u;
     }
-    for (uint32_t j = 0; j < 2; j += 1) {
-        const uint32_t e = e0 + j;
-        if (e < E) {
-            const uint32_t o = j == 0 ? o0 : o1;
-            if (a.off != nullptr) {
-                a.off[e] = o;
-            }
-            if (a.count != nullptr) {
-                a.count[e] = j == 0 ? c0 : c1;
-            }
-            uint32_t acc = o;
-            for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
-                uint32_t h[RB];
+    if (own0) {
+        if (a.off != nullptr) {
+            a.off[e0] = o0;
+        }
+        if (a.count != nullptr) {
+            a.count[e0] = c0;
+        }
+    }
+    if (own1) {
+        if (a.off != nullptr) {
+            a.off[e0 + 1] = o1;
+        }
+        if (a.count != nullptr) {
+            a.count[e0 + 1] = c1;
+        }
+    }
+    uint32_t acc0 = o0;
+    uint32_t acc1 = o1;
+    for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+        if (nb > RB) {
+            load_batch(bb0);
+        }
 #pragma unroll
-                for (uint32_t u = 0; u < RB; u += 1) {
-                    h[u] = bb0 + u < nb ? rmda_load_agent(&a.hist[(size_t)(bb0 + u) * E + e]) : 0u;
+        for (uint32_t u = 0; u < RB; u += 1) {
+            if (bb0 + u < nb) {
+                if (own0) {
+                    a.hist[(size_t)(bb0 + u) * E + e0] = acc0;
                 }
-#pragma unroll
-                for (uint32_t u = 0; u < RB; u += 1) {
-                    if (bb0 + u < nb) {
-                        a.hist[(size_t)(bb0 + u) * E + e] = acc;
-                    }
-                    acc += h[u];
+                if (own1) {
+                    a.hist[(size_t)(bb0 + u) * E + e0 + 1] = acc1;
                 }
             }
+            acc0 += h0[u];
+            acc1 += h1[u];
         }
     }
     if (a.items == nullptr) {
