@@ -47,6 +47,8 @@ def parse_args():
                     help="tokens in the CPU-baseline sample (default: sized for ~10-30 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true", help="skip re-measuring the copy and GEMM peaks")
+    ap.add_argument("--upload", action="store_true",
+                    help="also time rmda_moe_upload_layer from a bf16 safetensors file of this config's layer")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a device copy of known size (HBM counter calibration)")
     ap.add_argument("--stages", action="store_true", help="print the stage table to stderr")
@@ -154,6 +156,39 @@ def measure_peaks(torch):
     torch.cuda.empty_cache()
     return {"hbm_copy_GB/s": round(copy_gbs, 1), "hbm_copy": "1 GiB device copy, 2*bytes/t",
             "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
+
+
+def measure_upload(ctx, shape, torch):
+    """Write one layer's bf16 weights as safetensors (reference tensor names),
+    then time rmda_moe_upload_layer (mapped file -> pinned staging -> device ->
+    packed), three times so both staging banks are used."""
+    import tempfile
+    import numpy as np
+    from rmda_moe import st
+
+    prefix = "model.language_model.layers.0.mlp."
+    rng = np.random.default_rng(0)
+    ts = st.moe_layer_tensors(prefix, shape, rng)
+    nbytes = sum(a.nbytes for _, a in ts.values())
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "layer.safetensors")
+        st.write(path, ts)
+        del ts
+        with st.SafeTensors(path) as f:
+            packed = ctx.upload_layer(f, prefix, shape)  # first touch: maps pages, sizes the staging
+            ctx.upload_wait()
+            ctx.sync()
+            times = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ctx.upload_layer(f, prefix, shape, packed=packed)
+                ctx.upload_wait()
+                ctx.sync()
+                times.append(time.perf_counter() - t0)
+    best = min(times)
+    return {"GB/s": round(nbytes / best / 1e9, 2), "file_bytes": nbytes, "best_ms": round(best * 1e3, 2),
+            "what": "bf16 safetensors layer in the page cache -> pinned staging (host threads) -> device -> "
+                    "packed fp16, one rmda_moe_upload_layer + sync"}
 
 
 def main():
@@ -288,6 +323,7 @@ def main():
         print("calib copy: %d bytes read, %d bytes written per launch" % (n, n), file=sys.stderr)
 
     peaks = None if args.no_peaks else measure_peaks(torch)
+    upload = measure_upload(ctx, shape, torch) if args.upload else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -332,6 +368,8 @@ def main():
     }
     if cpu is not None:
         line["cpu_baseline"]["gpu_over_cpu"] = round(line["value"] / cpu["value"], 1)
+    if upload is not None:
+        line["upload"] = upload
     if peaks is not None:
         line["peaks_measured"] = peaks
         if roof["unit"] == "GB/s":

@@ -341,6 +341,68 @@ int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
                           const uint16_t *w_gate_up, const uint16_t *w_down, const uint16_t *w_sh_gate_up,
                           const uint16_t *w_sh_down, int bf16, uint16_t *packed);
 
+/* ---- safetensors weights (replaces src/safet.c: mda_safet_read, _tensor,
+ * _open_set, _find, :29-63,147-163,236-275) ---- */
+
+typedef struct rmda_st rmda_st_t;
+
+enum {
+    RMDA_ST_BF16 = 0,
+    RMDA_ST_F16 = 1,
+    RMDA_ST_F32 = 2,
+    RMDA_ST_I64 = 3,
+    RMDA_ST_I32 = 4,
+    RMDA_ST_U8 = 5,
+    RMDA_ST_OTHER = 15 /* indexed, but no element size is known */
+};
+#define RMDA_ST_MAX_DIMS 4
+
+typedef struct rmda_st_tensor_t {
+    const void *data; /* host pointer into the mapped file */
+    uint64_t bytes;
+    uint32_t dtype;   /* RMDA_ST_* */
+    uint32_t ndim;
+    uint64_t shape[RMDA_ST_MAX_DIMS];
+    uint32_t file;    /* shard index */
+} rmda_st_tensor_t;
+
+/* Map a .safetensors file, or a directory holding model.safetensors.index.json
+ * (every shard its weight_map names) or model.safetensors, and index the
+ * headers.  Offsets are checked against the data section and dtype x shape.
+ * Returns RMDA_OK or RMDA_ERR_ARG; rmda_st_message() says why (per thread). */
+int rmda_st_open(const char *path, rmda_st_t **out);
+void rmda_st_close(rmda_st_t *st);
+const char *rmda_st_message(void);
+uint32_t rmda_st_count(const rmda_st_t *st);
+const char *rmda_st_name(const rmda_st_t *st, uint32_t i);
+/* RMDA_ERR_ARG when no shard holds `name` (the reference's "missing"). */
+int rmda_st_find(const rmda_st_t *st, const char *name, rmda_st_tensor_t *out);
+
+/* ---- per-layer weight upload (replaces the staging banks, upload and
+ * qwen_bf16 conversion of src/qwen.c:228-247,366-394,441-452,1101-1134) ----
+ *
+ * Reads one layer's MoE tensors from `st`, named `prefix` + (the reference's
+ * names, src/qwen.c:441-452):
+ *   gate.weight                  [E][d]        bf16/f32 -> fp32 router rows
+ *   shared_expert_gate.weight    [1][d]        (shared > 0) router row E
+ *   experts.gate_up_proj         [E][2I][d]    bf16/f16 (or [E*2I][d])
+ *   experts.down_proj            [E][d][I]     bf16/f16 (or [E*d][I])
+ *   shared_expert.gate_proj.weight, .up_proj.weight [I_s][d], .down_proj.weight [d][I_s]
+ * e.g. prefix "model.language_model.layers.7.mlp.".  The bytes go from the
+ * mapped file into one of two pinned host staging banks, then with one
+ * asynchronous copy to device staging and through the pack kernels into
+ * `packed` (rmda_moe_packed_bytes(shape) bytes), all on the context's upload
+ * stream, so uploading layer l+1 overlaps computing layer l.  The call
+ * returns once the host copy is done and the device work is enqueued; a bank
+ * is reused only after its previous upload has finished.  Staging grows to
+ * the largest layer seen (this call may allocate; rmda_moe_layer never
+ * does).  Requires the same shape rules as rmda_moe_layer. */
+int rmda_moe_upload_layer(rmda_moe_ctx_t *ctx, const rmda_st_t *st, const char *prefix,
+                          const rmda_moe_shape_t *shape, uint16_t *packed);
+/* Make the context's compute stream wait for every upload enqueued so far
+ * (no host blocking). */
+int rmda_moe_upload_wait(rmda_moe_ctx_t *ctx);
+
 /* ---- stage profiler (replaces the reference's timestamp profiler:
  * mda_vkc_prof_begin / mda_vkc_prof_mark / mda_vkc_prof_report,
  * src/vkc.c:580-653, which writes a timestamp after every dispatch) ---- */

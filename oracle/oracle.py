@@ -13,6 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmoe_oracle.so")
 REF_HASH_PATH = os.path.join(HERE, "_ref", "libref_hash.so")
+REF_SAFET_PATH = os.path.join(HERE, "_ref", "libref_safet.so")
 
 NONE = 0xFFFFFFFF
 NO_SLOT = 0xFFFFFFFF
@@ -338,4 +339,43 @@ def ref_hash_lib():
     L.mda_hash_u64.argtypes = [ctypes.c_uint64] * 3
     L.mda_hash_mix.restype = ctypes.c_uint64
     L.mda_hash_mix.argtypes = [ctypes.c_uint64]
+    return L
+
+
+class RefSafetFile(ctypes.Structure):  # mda_safet_file_t, src/safet.h:24-30
+    _fields_ = [("bytes", _p), ("header", _p), ("data", _p), ("size", ctypes.c_uint64), ("mapped", ctypes.c_uint64)]
+
+
+class RefSafetTensor(ctypes.Structure):  # mda_safet_tensor_t, src/safet.h:32-38
+    _fields_ = [("data", _p), ("rows", _u32), ("cols", _u32), ("dtype", _u32), ("ok", ctypes.c_bool)]
+
+
+def ref_safet_lib():
+    """The reference's own src/safet.c built by oracle/Makefile, or None."""
+    if not os.path.exists(REF_SAFET_PATH):
+        return None
+    L = ctypes.CDLL(REF_SAFET_PATH)
+    L.mda_safet_read.restype = RefSafetFile
+    L.mda_safet_read.argtypes = [ctypes.c_char_p]
+    L.mda_safet_free.argtypes = [ctypes.POINTER(RefSafetFile)]
+    L.mda_safet_has.restype = ctypes.c_bool
+    L.mda_safet_has.argtypes = [ctypes.POINTER(RefSafetFile), ctypes.c_char_p]
+    L.mda_safet_tensor.restype = RefSafetTensor
+    L.mda_safet_tensor.argtypes = [ctypes.POINTER(RefSafetFile), ctypes.c_char_p]
+    return L
+
+
+class RefSafetSet(ctypes.Structure):  # mda_safet_set_t, src/safet.h:40-43
+    _fields_ = [("files", _p), ("n", _u32)]
+
+
+def ref_safet_set_api(L):
+    """Bind the reference's shard-set functions (src/safet.c:236-275)."""
+    L.mda_safet_open_set.restype = RefSafetSet
+    L.mda_safet_open_set.argtypes = [ctypes.c_char_p]
+    L.mda_safet_free_set.argtypes = [ctypes.POINTER(RefSafetSet)]
+    L.mda_safet_find.restype = RefSafetTensor
+    L.mda_safet_find.argtypes = [ctypes.POINTER(RefSafetSet), ctypes.c_char_p]
+    L.mda_safet_set_file.restype = _u32
+    L.mda_safet_set_file.argtypes = [ctypes.POINTER(RefSafetSet), ctypes.c_char_p]
     return L

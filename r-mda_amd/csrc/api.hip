@@ -8,6 +8,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <thread>
+#include <vector>
+
 #include "common.h"
 
 struct rmda_moe_ctx {
@@ -30,6 +34,16 @@ struct rmda_moe_ctx {
     uint32_t prof_layers;
     double prof_ms[RMDA_PROF_STAGES];
     hipEvent_t prof_ev[RMDA_PROF_RING][RMDA_PROF_STAGES + 1];
+    // weight upload: a stream of its own and two staging banks (pinned host +
+    // device), created at the first upload
+    int up_made;
+    hipStream_t up_stream;
+    uint32_t up_seq;
+    size_t up_cap;  // bytes per bank
+    uint8_t *up_host[2];
+    uint8_t *up_dev[2];
+    hipEvent_t up_done[2];  // bank b's last upload (copy + pack) finished
+    int up_used[2];
 };
 
 namespace {
@@ -267,6 +281,15 @@ void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
     }
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->up_made) {
+        (void)hipStreamSynchronize(ctx->up_stream);
+        for (int b = 0; b < 2; b += 1) {
+            (void)hipHostFree(ctx->up_host[b]);
+            (void)hipFree(ctx->up_dev[b]);
+            (void)hipEventDestroy(ctx->up_done[b]);
+        }
+        (void)hipStreamDestroy(ctx->up_stream);
+    }
     (void)hipFree(ctx->scratch);
     if (ctx->prof_made) {
         for (uint32_t i = 0; i < RMDA_PROF_RING; i += 1) {
@@ -814,6 +837,43 @@ size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape) {
     return plan_pack(shape).total * 2;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Enqueue every pack kernel of one layer on stream s; bf16 flags per tensor.
+int pack_layer(rmda_moe_ctx_t *ctx, hipStream_t s, const rmda_moe_shape_t *shape, const float *w_router,
+               const uint16_t *gu, int gu_bf16, const uint16_t *dn, int dn_bf16, const uint16_t *sgu, int sgu_bf16,
+               const uint16_t *sdn, int sdn_bf16, uint16_t *packed) {
+    const PackPlan pk = plan_pack(shape);
+    const uint32_t E = shape->experts, d = shape->d, I = shape->inter, S = shape->shared;
+    const int bk = (int)ctx->g2.bk;
+    int rc = hip_check(ctx, rmda_launch_pack(s, gu, packed + pk.gate_up, E, 2 * I, d, I, 1, bk, gu_bf16),
+                       "pack gate_up");
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_pack(s, dn, packed + pk.down, E, d, I, I, 0, bk, dn_bf16), "pack down");
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = hip_check(ctx, rmda_launch_pack(s, sgu, packed + pk.sh_gate_up, 1, 2 * S, d, S, 1, bk, sgu_bf16),
+                       "pack shared gate_up");
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = hip_check(ctx, rmda_launch_pack(s, sdn, packed + pk.sh_down, 1, d, S, S, 0, bk, sdn_bf16),
+                       "pack shared down");
+    }
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx,
+                       rmda_launch_router_pack(s, w_router, reinterpret_cast<float *>(packed + pk.router),
+                                               E + (S > 0 ? 1u : 0u), d),
+                       "pack router");
+    }
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
 int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const float *w_router,
                           const uint16_t *w_gate_up, const uint16_t *w_down, const uint16_t *w_sh_gate_up,
                           const uint16_t *w_sh_down, int bf16, uint16_t *packed) {
@@ -829,30 +889,245 @@ int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
     if (!check_shape(shape, why, sizeof(why))) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_pack_weights: %s", why);
     }
-    const PackPlan pk = plan_pack(shape);
-    const uint32_t E = shape->experts, d = shape->d, I = shape->inter, S = shape->shared;
-    const int bk = (int)ctx->g2.bk;
-    hipStream_t s = ctx->stream;
-    rc = hip_check(ctx, rmda_launch_pack(s, w_gate_up, packed + pk.gate_up, E, 2 * I, d, I, 1, bk, bf16),
-                   "pack gate_up");
+    return pack_layer(ctx, ctx->stream, shape, w_router, w_gate_up, bf16, w_down, bf16, w_sh_gate_up, bf16,
+                      w_sh_down, bf16, packed);
+}
+
+}  // extern "C"
+
+namespace {
+
+// One tensor of an upload: where it comes from and where it goes in a bank.
+struct UpPiece {
+    const uint8_t *src;
+    size_t bytes;
+    size_t dst;  // byte offset in the bank
+};
+
+uint64_t st_elems(const rmda_st_tensor_t &t) {
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < t.ndim; i += 1) {
+        n *= t.shape[i];
+    }
+    return n;
+}
+
+int up_find(rmda_moe_ctx_t *ctx, const rmda_st_t *st, const char *prefix, const char *suffix, uint64_t elems,
+            uint64_t last_dim, bool f32_ok, rmda_st_tensor_t *t) {
+    char name[512];
+    snprintf(name, sizeof(name), "%s%s", prefix, suffix);
+    if (rmda_st_find(st, name, t) != RMDA_OK) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_upload_layer: %s", rmda_st_message());
+    }
+    const bool dt_ok = t->dtype == RMDA_ST_BF16 || (f32_ok ? t->dtype == RMDA_ST_F32 : t->dtype == RMDA_ST_F16);
+    if (!dt_ok) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_upload_layer: %s has dtype code %u (want bf16 or %s)", name,
+                    t->dtype, f32_ok ? "f32" : "f16");
+    }
+    if (t->ndim == 0 || st_elems(*t) != elems || t->shape[t->ndim - 1] != last_dim) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_upload_layer: %s has %llu elements, last dim %llu; want %llu, %llu",
+                    name, (unsigned long long)st_elems(*t), (unsigned long long)t->shape[t->ndim - 1],
+                    (unsigned long long)elems, (unsigned long long)last_dim);
+    }
+    return RMDA_OK;
+}
+
+// Copy pieces into the pinned bank with up to 8 threads (page faults of the
+// mapped file dominate; they proceed in parallel).
+void up_copy(uint8_t *bank, const std::vector<UpPiece> &pieces) {
+    size_t total = 0;
+    for (const UpPiece &p : pieces) {
+        total += p.bytes;
+    }
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = std::max(1u, std::min(8u, nt));
+    if (total < ((size_t)64 << 20)) {
+        nt = 1;
+    }
+    const size_t chunk = (total + nt - 1) / nt;
+    auto work = [&](unsigned k) {
+        // thread k copies global byte range [k*chunk, (k+1)*chunk) of the concatenation
+        const size_t lo = (size_t)k * chunk;
+        const size_t hi = std::min(total, lo + chunk);
+        size_t base = 0;
+        for (const UpPiece &p : pieces) {
+            const size_t a = std::max(lo, base);
+            const size_t b = std::min(hi, base + p.bytes);
+            if (a < b) {
+                memcpy(bank + p.dst + (a - base), p.src + (a - base), b - a);
+            }
+            base += p.bytes;
+        }
+    };
+    if (nt == 1) {
+        work(0);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (unsigned k = 1; k < nt; k += 1) {
+        th.emplace_back(work, k);
+    }
+    work(0);
+    for (std::thread &t : th) {
+        t.join();
+    }
+}
+
+int up_reserve(rmda_moe_ctx_t *ctx, size_t bytes) {
+    if (!ctx->up_made) {
+        int rc = hip_check(ctx, hipStreamCreateWithFlags(&ctx->up_stream, hipStreamNonBlocking), "upload stream");
+        for (int b = 0; rc == RMDA_OK && b < 2; b += 1) {
+            rc = hip_check(ctx, hipEventCreateWithFlags(&ctx->up_done[b], hipEventDisableTiming), "upload event");
+        }
+        if (rc != RMDA_OK) {
+            return rc;
+        }
+        ctx->up_made = 1;
+    }
+    if (bytes <= ctx->up_cap) {
+        return RMDA_OK;
+    }
+    int rc = hip_check(ctx, hipStreamSynchronize(ctx->up_stream), "upload sync");
+    for (int b = 0; b < 2; b += 1) {
+        (void)hipHostFree(ctx->up_host[b]);
+        (void)hipFree(ctx->up_dev[b]);
+        ctx->up_host[b] = nullptr;
+        ctx->up_dev[b] = nullptr;
+        ctx->up_used[b] = 0;
+    }
+    ctx->up_cap = 0;
+    for (int b = 0; rc == RMDA_OK && b < 2; b += 1) {
+        rc = hip_check(ctx, hipHostMalloc(reinterpret_cast<void **>(&ctx->up_host[b]), bytes, hipHostMallocDefault),
+                       "pinned upload staging");
+        if (rc == RMDA_OK) {
+            rc = hip_check(ctx, hipMalloc(reinterpret_cast<void **>(&ctx->up_dev[b]), bytes), "device upload staging");
+        }
+    }
     if (rc == RMDA_OK) {
-        rc = hip_check(ctx, rmda_launch_pack(s, w_down, packed + pk.down, E, d, I, I, 0, bk, bf16), "pack down");
-    }
-    if (rc == RMDA_OK && S > 0) {
-        rc = hip_check(ctx, rmda_launch_pack(s, w_sh_gate_up, packed + pk.sh_gate_up, 1, 2 * S, d, S, 1, bk, bf16),
-                       "pack shared gate_up");
-    }
-    if (rc == RMDA_OK && S > 0) {
-        rc = hip_check(ctx, rmda_launch_pack(s, w_sh_down, packed + pk.sh_down, 1, d, S, S, 0, bk, bf16),
-                       "pack shared down");
-    }
-    if (rc == RMDA_OK) {
-        rc = hip_check(ctx,
-                       rmda_launch_router_pack(s, w_router, reinterpret_cast<float *>(packed + pk.router),
-                                               E + (S > 0 ? 1u : 0u), d),
-                       "pack router");
+        ctx->up_cap = bytes;
     }
     return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rmda_moe_upload_layer(rmda_moe_ctx_t *ctx, const rmda_st_t *st, const char *prefix,
+                          const rmda_moe_shape_t *shape, uint16_t *packed) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (st == nullptr || prefix == nullptr || shape == nullptr || packed == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_upload_layer: null argument");
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_upload_layer: %s", why);
+    }
+    const uint64_t E = shape->experts, d = shape->d, I = shape->inter, S = shape->shared;
+    rmda_st_tensor_t tr{}, tg{}, tgu{}, tdn{}, tsg{}, tsu{}, tsd{};
+    rc = up_find(ctx, st, prefix, "gate.weight", E * d, d, true, &tr);
+    if (rc == RMDA_OK && S > 0) {
+        rc = up_find(ctx, st, prefix, "shared_expert_gate.weight", d, d, true, &tg);
+    }
+    if (rc == RMDA_OK) {
+        rc = up_find(ctx, st, prefix, "experts.gate_up_proj", E * 2 * I * d, d, false, &tgu);
+    }
+    if (rc == RMDA_OK) {
+        rc = up_find(ctx, st, prefix, "experts.down_proj", E * d * I, I, false, &tdn);
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = up_find(ctx, st, prefix, "shared_expert.gate_proj.weight", S * d, d, false, &tsg);
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = up_find(ctx, st, prefix, "shared_expert.up_proj.weight", S * d, d, false, &tsu);
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = up_find(ctx, st, prefix, "shared_expert.down_proj.weight", d * S, S, false, &tsd);
+    }
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (S > 0 && tsg.dtype != tsu.dtype) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_upload_layer: shared gate_proj and up_proj dtypes differ");
+    }
+    // bank layout: router fp32 rows (E [+1]) x d, then the raw expert tensors
+    const uint64_t rows_r = E + (S > 0 ? 1 : 0);
+    const size_t off_r = 0;
+    const size_t off_gu = align256(off_r + rows_r * d * 4);
+    const size_t off_dn = align256(off_gu + tgu.bytes);
+    const size_t off_sgu = align256(off_dn + tdn.bytes);
+    const size_t off_sdn = align256(off_sgu + (S > 0 ? tsg.bytes + tsu.bytes : 0));
+    const size_t total = align256(off_sdn + (S > 0 ? tsd.bytes : 0));
+    rc = up_reserve(ctx, total);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    const uint32_t bank = ctx->up_seq % 2;
+    if (ctx->up_used[bank]) {
+        rc = hip_check(ctx, hipEventSynchronize(ctx->up_done[bank]), "wait for upload bank");
+        if (rc != RMDA_OK) {
+            return rc;
+        }
+    }
+    uint8_t *host = ctx->up_host[bank];
+    uint8_t *dev = ctx->up_dev[bank];
+    // router rows: bf16 widens exactly to fp32
+    float *rw = reinterpret_cast<float *>(host + off_r);
+    auto put_rows = [&](const rmda_st_tensor_t &t, float *dst, uint64_t n) {
+        if (t.dtype == RMDA_ST_F32) {
+            memcpy(dst, t.data, n * 4);
+        } else {
+            const uint16_t *b = static_cast<const uint16_t *>(t.data);
+            for (uint64_t i = 0; i < n; i += 1) {
+                const uint32_t u = (uint32_t)b[i] << 16;
+                memcpy(&dst[i], &u, 4);
+            }
+        }
+    };
+    put_rows(tr, rw, E * d);
+    if (S > 0) {
+        put_rows(tg, rw + E * d, d);
+    }
+    std::vector<UpPiece> pieces;
+    pieces.push_back({static_cast<const uint8_t *>(tgu.data), tgu.bytes, off_gu});
+    pieces.push_back({static_cast<const uint8_t *>(tdn.data), tdn.bytes, off_dn});
+    if (S > 0) {
+        // shared gate_up rows: the gate_proj rows, then the up_proj rows
+        pieces.push_back({static_cast<const uint8_t *>(tsg.data), tsg.bytes, off_sgu});
+        pieces.push_back({static_cast<const uint8_t *>(tsu.data), tsu.bytes, off_sgu + tsg.bytes});
+        pieces.push_back({static_cast<const uint8_t *>(tsd.data), tsd.bytes, off_sdn});
+    }
+    up_copy(host, pieces);
+    hipStream_t us = ctx->up_stream;
+    rc = hip_check(ctx, hipMemcpyAsync(dev, host, total, hipMemcpyHostToDevice, us), "upload copy");
+    if (rc == RMDA_OK) {
+        rc = pack_layer(ctx, us, shape, reinterpret_cast<const float *>(dev + off_r),
+                        reinterpret_cast<const uint16_t *>(dev + off_gu), tgu.dtype == RMDA_ST_BF16,
+                        reinterpret_cast<const uint16_t *>(dev + off_dn), tdn.dtype == RMDA_ST_BF16,
+                        reinterpret_cast<const uint16_t *>(dev + off_sgu), tsg.dtype == RMDA_ST_BF16,
+                        reinterpret_cast<const uint16_t *>(dev + off_sdn), tsd.dtype == RMDA_ST_BF16, packed);
+    }
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, hipEventRecord(ctx->up_done[bank], us), "upload event");
+    }
+    if (rc == RMDA_OK) {
+        ctx->up_used[bank] = 1;
+        ctx->up_seq += 1;
+    }
+    return rc;
+}
+
+int rmda_moe_upload_wait(rmda_moe_ctx_t *ctx) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK || !ctx->up_made || ctx->up_seq == 0) {
+        return rc;
+    }
+    // uploads run in order on the upload stream: the last one covers all
+    const uint32_t last = (ctx->up_seq - 1) % 2;
+    return hip_check(ctx, hipStreamWaitEvent(ctx->stream, ctx->up_done[last], 0), "wait for uploads");
 }
 
 int rmda_moe_fill_normal_f16(rmda_moe_ctx_t *ctx, uint16_t *dst, size_t n, uint64_t stream, uint64_t seed,

@@ -312,6 +312,8 @@ __global__ __launch_bounds__(256) void router_pack_kernel(const float *__restric
 
 uint32_t rmda_router_cpad(uint32_t cols) { return (cols + RMDA_WAVE - 1) / RMDA_WAVE * RMDA_WAVE; }
 
+namespace {
+
 template <int CG, bool FUSE>
 void launch_sx(hipStream_t s, dim3 grid, bool w_packed, const uint16_t *x16, const float *w, const float *bias,
                float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t cpad, uint32_t stride,
@@ -325,6 +327,8 @@ void launch_sx(hipStream_t s, dim3 grid, bool w_packed, const uint16_t *x16, con
                            d, cols, cpad, stride, nbias, zero_words, n_zero, fz);
     }
 }
+
+}  // namespace
 
 hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,

@@ -81,6 +81,15 @@ class LayerArgs(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t), ("packed", _p)]
 
 
+ST_BF16, ST_F16, ST_F32, ST_I64, ST_I32, ST_U8, ST_OTHER = 0, 1, 2, 3, 4, 5, 15
+ST_MAX_DIMS = 4
+
+
+class StTensor(ctypes.Structure):
+    _fields_ = [("data", _p), ("bytes", ctypes.c_uint64), ("dtype", _u32), ("ndim", _u32),
+                ("shape", ctypes.c_uint64 * ST_MAX_DIMS), ("file", _u32)]
+
+
 class WsLayout(ctypes.Structure):
     _fields_ = [("proj", ctypes.c_size_t), ("idx", ctypes.c_size_t), ("wt", ctypes.c_size_t),
                 ("count", ctypes.c_size_t), ("off", ctypes.c_size_t), ("slot", ctypes.c_size_t),
@@ -121,6 +130,14 @@ SIGNATURES = {
                                                 ctypes.c_float]),
     "rmda_moe_fill_normal_f32": (ctypes.c_int, [_p, _p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
                                                 ctypes.c_float]),
+    "rmda_st_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
+    "rmda_st_close": (None, [_p]),
+    "rmda_st_message": (ctypes.c_char_p, []),
+    "rmda_st_count": (_u32, [_p]),
+    "rmda_st_name": (ctypes.c_char_p, [_p, _u32]),
+    "rmda_st_find": (ctypes.c_int, [_p, ctypes.c_char_p, _p]),
+    "rmda_moe_upload_layer": (ctypes.c_int, [_p, _p, ctypes.c_char_p, _p, _p]),
+    "rmda_moe_upload_wait": (ctypes.c_int, [_p]),
 }
 
 _LIB = None

@@ -198,6 +198,22 @@ class Context:
                                                  1 if bf16 else 0, _ptr(packed)))
         return packed
 
+    def upload_layer(self, st, prefix, shape, packed=None):
+        """rmda_moe_upload_layer from a SafeTensors (rmda_moe.st) into `packed`
+        (allocated when None); returns it.  Enqueued on the upload stream."""
+        if packed is None:
+            n = packed_bytes(shape)
+            if n == 0:
+                raise ValueError("shape rejected by rmda_moe_packed_bytes: %r" % (shape,))
+            packed = torch.empty(n // 2, dtype=torch.float16, device="cuda")
+        s = shape_struct(shape)
+        self._check(self.L.rmda_moe_upload_layer(self.h, st.h, prefix.encode(), ctypes.byref(s), _ptr(packed)))
+        return packed
+
+    def upload_wait(self):
+        """The compute stream waits for every upload enqueued so far."""
+        self._check(self.L.rmda_moe_upload_wait(self.h))
+
     # ---- stage profiler ----
 
     def prof_begin(self):
