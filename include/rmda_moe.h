@@ -285,6 +285,16 @@ typedef struct rmda_moe_layer_args_t {
     const uint16_t *packed;     /* weights from rmda_moe_pack_weights, or NULL: then
                                    the kernels read w_router / w_gate_up / w_down /
                                    w_sh_* (the HF tensors above are ignored when set) */
+    /* Hyper-connection epilogue (src/qwen.c:887-906, shader/moe_combine.comp:36-38):
+     * with h != NULL the layer output y (fp32, before any rounding) is injected
+     * into hc residual streams in place,
+     *   h[r][s][c] += y[r][c] * 2 * sigmoid(inj[r*inj_stride + inj_off + s] / hc), s < hc,
+     * and `out` may be NULL (it is written only when given). */
+    float *h;                   /* rows x hc x d fp32, or NULL */
+    const float *inj;           /* rows x inj_stride fp32 injection logits */
+    uint32_t inj_stride;
+    uint32_t inj_off;
+    uint32_t hc;                /* 1 .. 8 streams (the reference uses 4) */
 } rmda_moe_layer_args_t;
 
 /* Device views into the workspace after rmda_moe_layer (byte offsets), so a

@@ -661,8 +661,14 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     }
     if (shape == nullptr || args == nullptr || args->x == nullptr || args->w_router == nullptr ||
         (args->packed == nullptr && (args->w_gate_up == nullptr || args->w_down == nullptr)) ||
-        args->out == nullptr || args->workspace == nullptr) {
+        (args->out == nullptr && args->h == nullptr) || args->workspace == nullptr) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: null argument");
+    }
+    if (args->h != nullptr &&
+        (args->inj == nullptr || args->hc == 0 || args->hc > RMDA_MAX_HC || args->inj_stride < args->inj_off + args->hc)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: hyper-connection streams need inj and 1 <= hc <= %u "
+                    "with inj_off + hc <= inj_stride (hc=%u, inj_off=%u, inj_stride=%u)", RMDA_MAX_HC, args->hc,
+                    args->inj_off, args->inj_stride);
     }
     char why[128];
     if (!check_shape(shape, why, sizeof(why))) {
@@ -810,11 +816,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_DOWN + 1);
     }
-    // A8/A9 combine (+ sigmoid-gated shared expert)
+    // A8/A9 combine (+ sigmoid-gated shared expert, + hyper-connection streams)
+    const rmda_hc_t hcp{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
                        rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.npairs, shape->shared > 0, args->out,
-                                             T, d, K),
+                                             T, d, K, &hcp),
                        "layer combine");
     }
     if (rc == RMDA_OK) {

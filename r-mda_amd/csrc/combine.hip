@@ -5,8 +5,8 @@
 // sigmoid(inj / hc)), plus a plain fp16 output mode.  One thread per output
 // element, like the reference.
 //
-// combine16_kernel is the fused layer's version: fp16 expert rows, plain fp16
-// output, one workgroup per token.  The token's topk (slot, weight) pairs are
+// combine16_kernel is the fused layer's version: fp16 expert rows, fp16
+// output and/or the hyper-connection streams, one workgroup per token.  The token's topk (slot, weight) pairs are
 // read once into LDS; each thread then handles 8 consecutive columns with
 // 16-byte loads of every selected row, accumulating in fp32 in j order (the
 // reference's order, :32-34) before the shared-expert term (:35).
@@ -53,6 +53,9 @@ __global__ __launch_bounds__(256) void combine_ref_kernel(rmda_pc_moe_combine_t 
     }
 }
 
+// HC: the hyper-connection epilogue of shader/moe_combine.comp:36-38 in place
+// of (or besides) the fp16 output: h[r][s][c] += acc * 2 * sigmoid(inj / hc).
+template <bool HC>
 __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict__ wt,
                                                         const uint32_t *__restrict__ slot,
                                                         const uint16_t *__restrict__ y,
@@ -60,9 +63,10 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
                                                         uint32_t pstride, uint32_t sg_off,
                                                         uint32_t shared_row0, int has_shared,
                                                         uint16_t *__restrict__ out, uint32_t d,
-                                                        uint32_t topk) {
+                                                        uint32_t topk, rmda_hc_t hcp) {
     __shared__ uint32_t s_slot[RMDA_MAX_TOPK + 1];
     __shared__ float s_wt[RMDA_MAX_TOPK + 1];
+    __shared__ float s_g[RMDA_MAX_HC];
     const uint32_t r = blockIdx.x;
     const uint32_t tid = threadIdx.x;
     if (tid < topk) {
@@ -72,6 +76,9 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
     if (tid == 0 && has_shared) {
         s_slot[RMDA_MAX_TOPK] = shared_row0 + r;
         s_wt[RMDA_MAX_TOPK] = sigmoidf(proj[(size_t)r * pstride + sg_off]);
+    }
+    if (HC && tid < hcp.hc) {
+        s_g[tid] = 2.0f * sigmoidf(hcp.inj[(size_t)r * hcp.inj_stride + hcp.inj_off + tid] / (float)hcp.hc);
     }
     __syncthreads();
     const uint32_t d8 = d / 8;
@@ -103,13 +110,33 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
                 acc[v] += wj * rmda_h2f(hv[v]);
             }
         }
-        uint4 o;
-        uint16_t *ov = reinterpret_cast<uint16_t *>(&o);
+        if (out != nullptr) {
+            uint4 o;
+            uint16_t *ov = reinterpret_cast<uint16_t *>(&o);
 #pragma unroll
-        for (int v = 0; v < 8; v += 1) {
-            ov[v] = rmda_f2h(acc[v]);
+            for (int v = 0; v < 8; v += 1) {
+                ov[v] = rmda_f2h(acc[v]);
+            }
+            reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = o;
         }
-        reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = o;
+        if (HC) {
+            for (uint32_t st = 0; st < hcp.hc; st += 1) {
+                float4 *hp = reinterpret_cast<float4 *>(hcp.h + ((size_t)r * hcp.hc + st) * d + (size_t)c * 8);
+                const float g = s_g[st];
+                float4 a = hp[0];
+                float4 b = hp[1];
+                a.x += acc[0] * g;
+                a.y += acc[1] * g;
+                a.z += acc[2] * g;
+                a.w += acc[3] * g;
+                b.x += acc[4] * g;
+                b.y += acc[5] * g;
+                b.z += acc[6] * g;
+                b.w += acc[7] * g;
+                hp[0] = a;
+                hp[1] = b;
+            }
+        }
     }
 }
 
@@ -130,11 +157,17 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
 hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
-                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk) {
+                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
+                                 const rmda_hc_t *hc) {
     if (rows == 0) {
         return hipSuccess;
     }
-    hipLaunchKernelGGL(combine16_kernel, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride, sg_off,
-                       shared_row0, has_shared, out, d, topk);
+    if (hc != nullptr && hc->h != nullptr) {
+        hipLaunchKernelGGL(combine16_kernel<true>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride, sg_off,
+                           shared_row0, has_shared, out, d, topk, *hc);
+    } else {
+        hipLaunchKernelGGL(combine16_kernel<false>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride,
+                           sg_off, shared_row0, has_shared, out, d, topk, rmda_hc_t{});
+    }
     return hipGetLastError();
 }

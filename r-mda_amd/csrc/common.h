@@ -252,10 +252,20 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
                                const uint32_t *slot, const float *y, const float *proj,
                                const float *sh, const float *inj, float *h, uint16_t *out);
 // fused-layer combine: y fp16 rows, optional shared rows at shared_row0 + r.
+// hyper-connection epilogue of the fused combine (h == NULL: none)
+struct rmda_hc_t {
+    float *h;
+    const float *inj;
+    uint32_t inj_stride;
+    uint32_t inj_off;
+    uint32_t hc;
+};
+#define RMDA_MAX_HC 8u
 hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
-                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk);
+                                 uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
+                                 const rmda_hc_t *hc);
 
 // elem.hip
 hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y);

@@ -78,7 +78,8 @@ class Shape(ctypes.Structure):
 class LayerArgs(ctypes.Structure):
     _fields_ = [("x", _p), ("w_router", _p), ("bias", _p), ("w_gate_up", _p), ("w_down", _p),
                 ("w_sh_gate_up", _p), ("w_sh_down", _p), ("out", _p), ("workspace", _p),
-                ("workspace_bytes", ctypes.c_size_t), ("packed", _p)]
+                ("workspace_bytes", ctypes.c_size_t), ("packed", _p), ("h", _p), ("inj", _p),
+                ("inj_stride", _u32), ("inj_off", _u32), ("hc", _u32)]
 
 
 ST_BF16, ST_F16, ST_F32, ST_I64, ST_I32, ST_U8, ST_OTHER = 0, 1, 2, 3, 4, 5, 15

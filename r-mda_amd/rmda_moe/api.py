@@ -177,11 +177,14 @@ class Context:
     # ---- fused layer ----
 
     def layer(self, shape, x, w_router, bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down, out, workspace,
-              packed=None):
+              packed=None, h=None, inj=None, inj_stride=0, inj_off=0, hc=0):
+        """rmda_moe_layer; with `h` (rows x hc x d fp32) the output is injected into
+        the hyper-connection streams (and `out` may be None)."""
         s = shape_struct(shape)
         args = LayerArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(w_gate_up), _ptr(w_down),
                          _ptr(w_sh_gate_up), _ptr(w_sh_down), _ptr(out), _ptr(workspace),
-                         workspace.numel() * workspace.element_size(), _ptr(packed))
+                         workspace.numel() * workspace.element_size(), _ptr(packed), _ptr(h), _ptr(inj),
+                         inj_stride, inj_off, hc)
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
 
     def pack_weights(self, shape, w_router, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, bf16=False,

@@ -91,6 +91,40 @@ def test_layer_other_seed_and_ragged(ctx):
     check_layer(ctx, cfg, seed=1)
 
 
+@pytest.mark.parametrize("cfg_id,n_sample", [(1, None), (5, 16)])
+def test_layer_hyper_connection_epilogue(ctx, cfg_id, n_sample):
+    """h[r][s][c] += y[r][c] * 2 * sigmoid(inj[r*stride + off + s] / hc)
+    (shader/moe_combine.comp:36-38), with y the fp32 layer output: checked
+    against the oracle's fp32 output in float64; `out` may be omitted."""
+    cfg = configs.CONFIGS[cfg_id]
+    inp = inputs.make_inputs(ctx, cfg, seed=4)
+    shape = inp["shape"]
+    T, d = shape["rows"], shape["d"]
+    hc, inj_stride, inj_off = 4, 11, 3
+    g = torch.Generator(device="cuda").manual_seed(9)
+    h0 = torch.randn(T, hc, d, device="cuda", generator=g)
+    inj = torch.randn(T, inj_stride, device="cuda", generator=g) * 3
+    h = h0.clone()
+    ws = inputs.workspace_for(shape)
+    ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
+              inp["w_sh_gate_up"], inp["w_sh_down"], None, ws, h=h, inj=inj, inj_stride=inj_stride,
+              inj_off=inj_off, hc=hc)
+    ctx.sync()
+    host = inputs.to_host(inp)
+    sel = None
+    if n_sample:
+        sel = np.sort(np.random.default_rng(2).choice(T, n_sample, replace=False)).astype(np.uint32)
+    ref = orc.layer(host, tile=1, rows_sel=sel)
+    rows = np.arange(T) if sel is None else sel.astype(np.int64)
+    gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[rows, inj_off:inj_off + hc] / hc))
+    want = h0.cpu().numpy()[rows].astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]
+    got = h.cpu().numpy()[rows].astype(np.float64)
+    err = np.abs(got - want).max()
+    print("  hc max-abs %.3g" % err, flush=True)
+    assert err <= 2 * MAX_ABS, err
+    assert torch.isfinite(h).all()
+
+
 def test_layer_zero_rows_is_a_no_op(ctx):
     """rows = 0 (an empty chunk) enqueues nothing harmful and returns OK."""
     cfg = dict(configs.CONFIGS[3], rows=0, name="empty")
