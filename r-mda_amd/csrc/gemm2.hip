@@ -28,6 +28,10 @@
 //     instruction reads one contiguous KiB and a whole stage of B is one
 //     contiguous 16 KiB block (the HF [out][in] layout would read BK-wide
 //     pieces of 256 rows 4 KiB apart).
+//   * Weight loads carry the non-temporal hint: every weight byte is read
+//     once per launch, and keeping it out of the caches leaves them to the
+//     gathered activation rows and to the next kernel's inputs (gate_up
+//     176 vs 178 us, combine 14.7 vs 15.6 us at BASELINE config 3).
 //   * The grid is renumbered XCD-aware from the real work count read on the
 //     device: XCD x gets a contiguous range of (item, N tile) pairs, so the N
 //     tiles of one item (which share A rows) meet in one L2 and the 8 XCDs
@@ -128,7 +132,7 @@ __device__ __forceinline__ void wait_stage(bool live, bool b_hi, uint32_t after)
 // each wait is exact or conservative.
 typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
 
-template <int MODE, int BN, int BK, int STAGES, bool PACKED>
+template <int MODE, int BN, int BK, int STAGES, bool PACKED, int BPOL>
 __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t MB = BM / 64;             // row blocks
     constexpr uint32_t NB = BN / 64;             // column blocks
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
         } else if (q - A_PER < n_b) {
             const uint32_t j = q - A_PER;
             const uint16_t *src = PACKED ? b_src[j] + (size_t)i_s * (SLAB * BK) : b_src[j] + i_s * BK;
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)(ibase + b_dst[j]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)(ibase + b_dst[j]), 16, 0, BPOL);
         }
     };
     auto issue_end = [&]() __attribute__((always_inline)) { i_s += 1; };
@@ -504,12 +508,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t *__restrict__ 
     }
 }
 
-template <int MODE, int BN, int BK, int STAGES>
+template <int MODE, int BN, int BK, int STAGES, int BPOL>
 hipError_t launch_cfg(hipStream_t s, const rmda_gemm_args_t *a, dim3 grid, bool packed) {
     if (packed) {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true>), grid, dim3(BM / 64 * BN), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true, BPOL>), grid, dim3(BM / 64 * BN), 0, s, *a);
     } else {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false>), grid, dim3(BM / 64 * BN), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false, BPOL>), grid, dim3(BM / 64 * BN), 0, s, *a);
     }
     return hipGetLastError();
 }
@@ -523,12 +527,12 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
     const dim3 grid(wgs);
     if (c.stages == 4) {
-        return launch_cfg<MODE, 256, 32, 4>(s, a, grid, packed);
+        return launch_cfg<MODE, 256, 32, 4, 2>(s, a, grid, packed);
     }
-    if (c.stages == 3) {
-        return launch_cfg<MODE, 256, 32, 3>(s, a, grid, packed);
+    if (c.bpol == 0) {
+        return launch_cfg<MODE, 256, 32, 5, 0>(s, a, grid, packed);
     }
-    return launch_cfg<MODE, 256, 32, 5>(s, a, grid, packed);
+    return launch_cfg<MODE, 256, 32, 5, 2>(s, a, grid, packed);
 }
 
 }  // namespace
@@ -537,9 +541,9 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
 // the benchmark shapes.  LDS per workgroup = STAGES * (192 + BN) * BK * 2.
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     switch (variant) {
-    case 1: return {256, 32, 4, 0};
-    case 2: return {256, 32, 3, 0};
-    default: return {256, 32, 5, 0};
+    case 1: return {256, 32, 4, 0, 2};
+    case 2: return {256, 32, 5, 0, 0};
+    default: return {256, 32, 5, 0, 2};
     }
 }
 
