@@ -340,9 +340,10 @@ size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape);
  * w_sh_down [d][I_s] when shared > 0) into the order the kernels stream
  * them.  Each 256-row x K-step expert-weight slab becomes one contiguous
  * block in exactly the layout the grouped GEMM keeps it in LDS, so every
- * weight load is a contiguous KiB; the router matrix becomes [d/4][cols][4]
- * so that one wave's router-weight load (64 columns x 4 k) is a contiguous
- * KiB.  With bf16 != 0 the expert weights are bf16 and are converted to
+ * weight load is a contiguous KiB; the router matrix becomes
+ * [d/16][cols rounded up to 64][4][4], element (k, c) at
+ * ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4, so that one wave's load of a
+ * 16-column MFMA tile for 16 k is a contiguous KiB.  With bf16 != 0 the expert weights are bf16 and are converted to
  * fp16 (round to nearest even) on the way, in place of qwen_bf16; the router
  * matrix is copied exactly.  Enqueued on the context stream; `packed` must
  * hold rmda_moe_packed_bytes(shape) bytes and must not overlap the inputs.

@@ -126,16 +126,15 @@ __device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts,
     }
 }
 
-// Router kernel with the top-k fused in: one workgroup owns all logits of
-// RMDA_ROUTE_GROUP tokens (cols <= rmda_route_fuse_max_cols()) and routes
-// them from LDS.
+// Router kernel with the top-k fused in: when one workgroup's column slice
+// covers the row (cols <= rmda_route_fuse_max_cols()), it routes its
+// tokens from LDS.
 struct rmda_route_fuse_t {
     uint32_t experts;
     uint32_t topk;
     uint32_t *idx;       // [rows][topk]
     float *wt;           // [rows][topk]
 };
-#define RMDA_ROUTE_GROUP 8u
 uint32_t rmda_route_fuse_max_cols();
 
 // ---- launch helpers implemented by the kernel files ----
@@ -147,7 +146,8 @@ hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
                               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
                               const rmda_route_fuse_t *fuse);
-// Packed router weights: [d/4][rmda_router_cpad(cols)][4] fp32.
+// Packed router weights: [d/16][rmda_router_cpad(cols)][4][4] fp32, element
+// (k, c) at ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4.
 uint32_t rmda_router_cpad(uint32_t cols);
 hipError_t rmda_launch_router_pack(hipStream_t s, const float *w, float *out, uint32_t cols, uint32_t d);
 

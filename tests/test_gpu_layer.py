@@ -177,10 +177,14 @@ def test_pack_bf16_input_equals_fp16_of_converted(ctx):
     a = np.sort(p_h.view(torch.int16).cpu().numpy()[:n_exp])
     b = np.sort(np.concatenate([gu16.view(np.int16).ravel(), dn16.view(np.int16).ravel()]))
     assert np.array_equal(a, b)
-    # the router matrix follows as [d/4][cols rounded up to 64][4] fp32, zero padded, bits unchanged
+    # the router matrix follows as [d/16][cols rounded up to 64][4][4] fp32, zero padded, bits
+    # unchanged: element (k, c) at ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4
     cpad = (E + 63) // 64 * 64
     rt = p_h[n_exp:].view(torch.float32).cpu().numpy()
     assert rt.size == d * cpad
-    want = np.zeros((d // 4, cpad, 4), np.float32)
-    want[:, :E, :] = wr.cpu().numpy().reshape(E, d // 4, 4).transpose(1, 0, 2)
+    want = np.zeros((d // 16, cpad, 4, 4), np.float32)
+    # w[c][16g + 4s + kk] -> want[g][c][kk][s]
+    want[:, :E] = wr.cpu().numpy().reshape(E, d // 16, 4, 4).transpose(1, 0, 3, 2)
     assert np.array_equal(rt.view(np.uint32), want.reshape(-1).view(np.uint32))
+    k, c = 37, 5  # one element by the formula
+    assert rt[((k // 16) * cpad + c) * 16 + (k % 4) * 4 + (k % 16) // 4] == wr[c, k].item()
