@@ -41,13 +41,34 @@ __device__ __forceinline__ float rmda_key_float(uint32_t k) {
     return __builtin_bit_cast(float, u);
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t rmda_dpp_u64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)v, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t rmda_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Maximum over the wave, returned to every lane; the whole wave must be
+// active.  Register-only: DPP within each 16-lane row (swap neighbours, swap
+// pairs, mirror halves, mirror the row), then v_permlane16_swap and
+// v_permlane32_swap exchange rows and halves, so no step goes through the
+// LDS pipeline the way a generic lane shuffle (ds_bpermute) does.
 __device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)v, m);
-        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
-        uint64_t o = ((uint64_t)hi << 32) | lo;
-        v = o > v ? o : v;
+    v = rmda_max_u64(v, rmda_dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = rmda_max_u64(v, rmda_dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]: quad max
+    v = rmda_max_u64(v, rmda_dpp_u64<0x141>(v));  // row_half_mirror: 8-lane max
+    v = rmda_max_u64(v, rmda_dpp_u64<0x140>(v));  // row_mirror: row max
+    {
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        v = rmda_max_u64(((uint64_t)hi[0] << 32) | lo[0], ((uint64_t)hi[1] << 32) | lo[1]);  // 32-lane max
+    }
+    {
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        v = rmda_max_u64(((uint64_t)hi[0] << 32) | lo[0], ((uint64_t)hi[1] << 32) | lo[1]);  // wave max
     }
     return v;
 }
