@@ -68,6 +68,48 @@ def test_router_bitexact(ctx, rows, d, cols, stride, bias):
     assert np.all(got[:, cols:] == 7.0), "columns beyond cols must stay untouched"
 
 
+def test_router_special_values_bitexact(ctx):
+    """The matrix-core router against fmaf on the values where an MFMA could
+    differ from IEEE fused multiply-adds: subnormal products and partial sums
+    (tiny activations x tiny weights, subnormal weights), exact cancellation
+    to signed zeros, overflow to infinity, and infinities / NaN inputs.
+    Non-NaN logits must match bitwise; NaN must appear exactly where the
+    oracle has NaN (its payload is not compared)."""
+    rows, d, cols = 48, 2048, 40
+    r = rng(11)
+    x = r.standard_normal((rows, d)).astype(np.float16)
+    w = (r.standard_normal((cols, d)) * 0.02).astype(np.float32)
+    x[0:8] = (r.standard_normal((8, d)) * 3e-5).astype(np.float16)  # includes fp16 subnormals
+    w[0:8] = (r.standard_normal((8, d)) * 1e-34).astype(np.float32)  # tiny x tiny -> subnormal products
+    w[8:12] = (r.standard_normal((4, d)) * 1e-39).astype(np.float32)  # subnormal weights
+    # cancellation: each chunk's second half repeats the first half negated -> exact zeros, sign per rounding
+    L = d // 8
+    for c in range(12, 16):
+        for q in range(8):
+            half = w[c, q * L:q * L + L // 2].copy()
+            w[c, q * L + L // 2:(q + 1) * L] = -half
+            x[16:24, q * L + L // 2:(q + 1) * L] = x[16:24, q * L:q * L + L // 2]
+    x[24:28, :] = np.float16(-0.0)  # all-negative-zero activations
+    x[40, 5] = np.float16(np.inf)
+    x[41, 7] = np.float16(-np.inf)
+    w[20, 5] = 0.0                   # inf * 0 -> NaN in column 20 of row 40
+    x[42, :] = np.float16(60000.0)
+    w[21, :] = 1e35                  # overflow to +inf
+    w[22, :] = -1e35                 # overflow to -inf
+    x[43, 9] = np.float16(np.nan)
+    ref = orc.router(x.view(np.uint16), w, None, nbias=0, stride=cols)
+    proj = torch.full((rows, cols), 7.0, dtype=torch.float32, device="cuda")
+    ctx.router(rows, d, cols, cols, 0, dev(x.view(np.uint16)), dev(w), None, proj)
+    ctx.sync()
+    got = proj.cpu().numpy()
+    nan = np.isnan(ref)
+    assert nan.any() and np.isinf(ref).any() and (ref == 0).any(), "the planted cases must occur"
+    sub = (ref != 0) & (np.abs(ref) < np.finfo(np.float32).tiny)
+    assert sub.any(), "some logits must be subnormal"
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
 # ---------------------------------------------------------------- route (A1)
 
 def planted_logits(rows, experts, stride, seed):
