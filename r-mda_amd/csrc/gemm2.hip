@@ -306,6 +306,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     uint32_t kc = 0;  // compute task ordinal and K step
     uint32_t ks = 0;
     bool live = false;
+    uint32_t nlive = 0;  // 16-row blocks of this wave's 64 rows that hold task rows
     constexpr uint32_t KK = BK / 32;
     typedef half8_t frag_t[KK][4];
     frag_t fa0, fb0;
@@ -330,6 +331,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
             c_row0 = items[item * 4 + 1];
             c_rows = items[item * 4 + 2];
             live = wm * 64 < c_rows;
+            nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
 #pragma unroll
             for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -400,9 +402,9 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     };
     auto compute = [&](const frag_t &fa, const frag_t &fb) __attribute__((always_inline)) {
         compute_begin();
-        if (live) {
 #pragma unroll
-            for (int i = 0; i < 4; i += 1) {
+        for (int i = 0; i < 4; i += 1) {
+            if ((uint32_t)i < nlive) {
                 mfma_group(fa, fb, i);
             }
         }
@@ -444,7 +446,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
         ibuf = ibuf + 1 == STAGES ? 0 : ibuf + 1;
 #pragma unroll
         for (int i = 0; i < 4; i += 1) {
-            if (live) {
+            if ((uint32_t)i < nlive) {
                 mfma_group(fa0, fb0, i);
             }
             if ((uint32_t)i < A_PER + B_HI) {
