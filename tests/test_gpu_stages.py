@@ -53,6 +53,9 @@ def test_fill_matches_oracle_bitwise(ctx, n, stream, seed, std):
     (37, 2048, 70, 72, True),       # d = 2048 kernel: shifted last token tile, partial column group
     (23, 2048, 513, 513, True),     # d = 2048 kernel, one column in the last group
     (5, 2048, 128, 128, False),     # fewer rows than one token tile
+    (37, 384, 70, 72, True),        # 3 sub-tiles of 16 k per chunk: the 4-slot ring's tail step
+    (64, 128, 40, 40, False),       # one sub-tile per chunk
+    (100, 1152, 33, 33, True),      # 9 sub-tiles per chunk; 33 columns: a second column block of one
 ])
 def test_router_bitexact(ctx, rows, d, cols, stride, bias):
     x = orc.fill_normal_f16(rows * d, configs.STREAM_X, 1, 1.0).reshape(rows, d)
