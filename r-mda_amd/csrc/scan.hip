@@ -26,14 +26,16 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t *p, size_t n, uint32
 __device__ uint32_t block_exscan(uint32_t v, uint32_t *sbuf, uint32_t *total) {
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
     const uint32_t w = threadIdx.x / RMDA_WAVE;
+    // inclusive wave scan in registers: DPP row_shr 1, 2, 4, 8 within each
+    // 16-lane row (lanes shifted in from outside the row add 0), then
+    // row_bcast 15 and 31 carry the row totals upward
     uint32_t x = v;
-#pragma unroll
-    for (int o = 1; o < RMDA_WAVE; o <<= 1) {
-        uint32_t y = __shfl_up(x, o);
-        if (lane >= (uint32_t)o) {
-            x += y;
-        }
-    }
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xC, 0xF, false);
     if (lane == RMDA_WAVE - 1) {
         sbuf[w] = x;
     }
@@ -110,19 +112,23 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         run[e] = 0;
     }
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (RMDA_WAVE - lane));
-    for (uint32_t it = 0; it < RMDA_RANK_BLOCK / NT; it += 1) {
+    // all of the thread's experts are loaded up front: one memory round trip
+    // for the block instead of one per 256 pairs
+    constexpr uint32_t ITS = RMDA_RANK_BLOCK / NT;
+    uint32_t ev[ITS];
+#pragma unroll
+    for (uint32_t it = 0; it < ITS; it += 1) {
+        const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
+        ev[it] = pr < a.npairs ? a.idx[pr] : RMDA_NONE;
+    }
+#pragma unroll
+    for (uint32_t it = 0; it < ITS; it += 1) {
         for (uint32_t e = lane; e < E; e += RMDA_WAVE) {
             msk[w][e] = 0ull;
         }
         __syncthreads();
         const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
-        uint32_t e = RMDA_NONE;
-        if (pr < a.npairs) {
-            e = a.idx[pr];
-            if (e >= E) {
-                e = RMDA_NONE;
-            }
-        }
+        const uint32_t e = ev[it] < E ? ev[it] : RMDA_NONE;
         if (e != RMDA_NONE) {
             atomicOr(&msk[w][e], 1ull << lane);
         }
