@@ -258,6 +258,7 @@ struct rmda_gemm2_cfg_t {
     uint32_t stages;
     uint32_t grid;  // persistent workgroups (the device's CU count)
     uint32_t bpol;  // cache-policy bits of the weight (B) loads: 2 = non-temporal (streamed once)
+    uint32_t spec;  // dedicated load-issue waves (0: every MFMA wave issues its share)
 };
 // rows of padding after the gathered-row index buffer (rowtok) that the
 // grouped GEMM's scalar index reads may touch

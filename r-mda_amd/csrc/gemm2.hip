@@ -7,16 +7,15 @@
 // from HBM (arithmetic intensity ~120 FLOP/B against a ridge of ~312).  Two
 // things decide the speed: every weight byte leaves HBM once, and enough
 // bytes are in flight to cover HBM latency.
-//   * A work item is (group, first row, up to 256 rows): one workgroup owns
-//     all rows of an expert (up to 256) for one BN-wide N tile, so each
-//     weight tile is read once.  The 256 rows are four 64-row blocks; a block
-//     past the item's end loads no A rows and runs no MFMAs (tile height
-//     follows the expert's load at 64-row grain).
+//   * A work item is (group, first row, up to 192 rows): one workgroup owns
+//     all rows of an expert (up to 192) for one 256-wide N tile, so each
+//     weight tile is read once.  The 192 rows are three 64-row blocks; a
+//     16-row MFMA group past the item's end runs no MFMAs.
 //   * Operand tiles go straight from global memory into LDS with gfx950's
 //     global_load_lds_dwordx4 (no register staging), through a ring of
-//     STAGES buffers; while stage s is multiplied, the next STAGES-1 stages
-//     are in flight.  Completion is tracked per wave with explicit vmcnt
-//     waits (each wave knows how many loads it issued per stage) and a bare
+//     STAGES buffers, so several stages are in flight while one is
+//     multiplied.  Completion is tracked with explicit vmcnt waits (each
+//     issuing wave knows how many loads it issued per stage) and a bare
 //     s_barrier, so no compiler-inserted full wait drains the pipeline.
 //   * LDS rows are BK halves; the 16-byte chunks of row r sit XOR-swizzled
 //     (swz below) so MFMA fragment reads are free of bank conflicts.  A DMA
@@ -36,8 +35,20 @@
 //     device: XCD x gets a contiguous range of (item, N tile) pairs, so the N
 //     tiles of one item (which share A rows) meet in one L2 and the 8 XCDs
 //     get equal shares whatever the routing.
-// MFMA: v_mfma_f32_16x16x32_f16, fp32 accumulate; 8 waves = 4 (M) x 2 (N),
-// 64 x BN/2 per wave.
+// MFMA: v_mfma_f32_16x16x32_f16, fp32 accumulate; 12 MFMA waves = 3 (M) x
+// 4 (N), 64 x 64 per wave.
+//
+// Two kernels share this design:
+//   * gemm2_kernel: every MFMA wave also issues its share of each stage's
+//     DMA, between its MFMA groups (HF-layout weights, and measurement
+//     variants for packed ones).
+//   * gemm3_kernel (packed weights, the default): four more waves issue all
+//     of the DMA and nothing else, so a stage's loads leave right after the
+//     stage barrier instead of queueing behind MFMAs; for gate_up a second
+//     barrier after the fragment reads frees a buffer before its MFMAs run,
+//     so all STAGES buffers are in flight.  Measured at config 3 against
+//     gemm2_kernel on the same boxes: gate_up 175.3 -> 172.6 us, down
+//     106.1 -> 104.9 us (the second barrier helps gate_up, not down).
 #include "common.h"
 
 namespace {
@@ -472,6 +483,262 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     }
 }
 
+// Dedicated-issue variant: the 12 MFMA waves issue no loads; NDW more waves
+// issue every stage's DMA (A rows and packed B slabs) and do nothing else.
+// Each stage: the issue waves wait for their loads of stage g (exact vmcnt:
+// every issue wave issues the same L_PER loads per stage), all waves meet
+// at the stage barrier, then the issue waves put stage g + STAGES - 1 into
+// the buffer stage g - 1 used while the MFMA waves multiply stage g.  So a
+// stage's loads go out right after the barrier instead of between MFMA
+// groups, and no MFMA wave waits on vmcnt.  Packed weights only.
+template <int MODE, int STAGES, int BPOL, int NDW, bool DB>
+__global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
+    constexpr uint32_t BN = 256;
+    constexpr uint32_t BK = 32;
+    constexpr uint32_t MB = BM / 64;
+    constexpr uint32_t NB = BN / 64;
+    constexpr uint32_t NMW = MB * NB;           // 12 MFMA waves
+    constexpr uint32_t CH = BK / 8;             // 16-byte chunks per row
+    constexpr uint32_t RPI = 64 / CH;           // rows per wave-wide DMA instruction
+    constexpr uint32_t A_BYTES = BM * BK * 2;
+    constexpr uint32_t B_BYTES = BN * BK * 2;
+    constexpr uint32_t STAGE_BYTES = A_BYTES + B_BYTES;
+    constexpr uint32_t A_PER = BM / RPI / NDW;  // A instructions per issue wave per stage
+    constexpr uint32_t B_PER = BN / RPI / NDW;  // B instructions per issue wave per stage
+    constexpr uint32_t L_PER = A_PER + B_PER;
+    constexpr uint32_t AROWS = A_PER * RPI;     // A rows per issue wave
+    static_assert(BM / RPI % NDW == 0 && BN / RPI % NDW == 0, "issue waves split a stage evenly");
+    static_assert(AROWS <= 48, "gathered rows per issue wave");
+    static_assert((NMW + NDW) * RMDA_WAVE <= 1024, "workgroup size");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % RMDA_WAVE;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
+
+    // ---- this workgroup's tasks: XCD x owns a contiguous, equal share ----
+    const_u32p items = (const_u32p)g.items;
+    const uint32_t n_slabs = g.n_w / SLAB;
+    const uint32_t ntiles = n_slabs / (BN / SLAB);
+    const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
+    const uint32_t total = n_items * ntiles;
+    const uint32_t per = (total + 7) / 8;
+    const uint32_t xcd = blockIdx.x % 8;
+    const uint32_t stride = gridDim.x / 8;
+    const uint32_t first = xcd * per + blockIdx.x / 8;
+    const uint32_t last = min((xcd + 1) * per, total);
+    if (first >= last) {
+        return;
+    }
+    const uint32_t ntask = (last - first + stride - 1) / stride;
+    const uint32_t steps = g.k / BK;
+    const uint32_t nstage = ntask * steps;
+
+    if (w >= NMW) {
+        // ================= issue waves =================
+        const uint32_t dw = w - NMW;
+        const uint32_t lrow = lane / CH;
+        const uint32_t lch = lane % CH;
+        const uint16_t *a_src[A_PER];
+        const uint16_t *b_src[B_PER];
+        auto setup = [&](uint32_t k) __attribute__((always_inline)) {
+            const uint32_t task = first + k * stride;
+            const uint32_t item = task / ntiles;
+            const uint32_t nt = task % ntiles;
+            const uint32_t grp = items[item * 4 + 0];
+            const uint32_t row0 = items[item * 4 + 1];
+            const uint32_t rows = items[item * 4 + 2];
+            const bool is_shared = grp == g.shared_group;
+            const uint16_t *wg = is_shared ? g.w_shared : g.w + (size_t)grp * g.n_w * g.k;
+            const uint32_t rbase = dw * AROWS;
+#pragma unroll
+            for (uint32_t j = 0; j < A_PER; j += 1) {
+                const uint32_t r = rbase + j * RPI + lrow;
+                const uint32_t rr = r < rows ? r : 0u;
+                uint32_t arow;
+                if (MODE == RMDA_GEMM_SWIGLU) {
+                    if (is_shared) {
+                        arow = row0 + rr - g.shared_row0;
+                    } else {
+                        // gathered token rows (scalar loads; the index buffer is
+                        // padded so these reads never leave it)
+                        const const_u32p rt = (const_u32p)g.rowtok + row0 + rbase + j * RPI;
+                        uint32_t tok[RPI];
+#pragma unroll
+                        for (uint32_t c = 0; c < RPI; c += 1) {
+                            tok[c] = rt[c];
+                        }
+                        uint32_t t = tok[0];
+#pragma unroll
+                        for (uint32_t c = 1; c < RPI; c += 1) {
+                            t = lrow == c ? tok[c] : t;
+                        }
+                        arow = r < rows ? t : ((const_u32p)g.rowtok + row0)[0];
+                    }
+                } else {
+                    arow = row0 + rr;
+                }
+                a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                const uint32_t nbase = (dw * B_PER + j) * RPI;
+                const uint32_t slab = nt * (BN / SLAB) + nbase / SLAB;
+                const uint32_t nin = nbase % SLAB;
+                b_src[j] = wg + (size_t)slab * steps * (SLAB * BK) + nin * BK + lane * 8;
+            }
+        };
+        uint32_t i_task = 0;
+        uint32_t i_s = 0;
+        setup(0);
+        auto issue = [&](uint32_t buf) __attribute__((always_inline)) {
+            if (i_s == steps) {
+                i_task += 1;
+                i_s = 0;
+                setup(i_task);
+            }
+            uint8_t *base = smem + buf * STAGE_BYTES;
+#pragma unroll
+            for (uint32_t j = 0; j < A_PER; j += 1) {
+                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + i_s * BK),
+                                                 (lds_void_t *)(base + (dw * AROWS + j * RPI) * (BK * 2)), 16, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (size_t)i_s * (SLAB * BK)),
+                                                 (lds_void_t *)(base + A_BYTES + (dw * B_PER + j) * RPI * (BK * 2)),
+                                                 16, 0, BPOL);
+            }
+            i_s += 1;
+        };
+        // DB: a second barrier per stage, after the MFMA waves have read the
+        // stage's fragments into registers, frees its buffer before the
+        // MFMAs run, so all STAGES buffers can be in flight
+        constexpr uint32_t AHEAD = DB ? STAGES : STAGES - 1;
+#pragma unroll
+        for (uint32_t s = 0; s < AHEAD; s += 1) {
+            if (s < nstage) {
+                issue(s);
+            }
+        }
+        uint32_t ibuf = AHEAD % STAGES;
+        for (uint32_t gs = 0; gs < nstage; gs += 1) {
+            const uint32_t later = min(nstage - 1 - gs, AHEAD - 1);
+            wait_after<L_PER>(later);
+            __builtin_amdgcn_s_barrier();
+            if (DB) {
+                __builtin_amdgcn_s_barrier();
+            }
+            if (gs + AHEAD < nstage) {
+                issue(ibuf);
+                ibuf = ibuf + 1 == STAGES ? 0 : ibuf + 1;
+            }
+        }
+        return;
+    }
+
+    // ================= MFMA waves =================
+    const uint32_t wm = w / NB;
+    const uint32_t wn = w % NB;
+    const uint32_t fr = lane % 16;
+    const uint32_t fq = lane / 16;
+    const uint32_t ch_off = (fq ^ swz<BK>(fr)) * 16;
+    const uint32_t a_row_off = (wm * 64 + fr) * (BK * 2);
+    const uint32_t b_row_off = A_BYTES + (wn * 64 + fr) * (BK * 2);
+    const uint32_t rq = 4 * fq;
+    floatx4_t acc[4][4];
+    uint32_t c_row0 = 0;
+    uint32_t c_rows = 0;
+    uint32_t c_nt = 0;
+    uint32_t kc = 0;
+    uint32_t ks = 0;
+    bool live = false;
+    uint32_t nlive = 0;
+    uint32_t cbuf = 0;
+    for (uint32_t gs = 0; gs < nstage; gs += 1) {
+        lds_barrier();
+        const uint8_t *base = smem + cbuf * STAGE_BYTES;
+        cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
+        half8_t fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            fa[i] = *reinterpret_cast<const half8_t *>(base + a_row_off + i * 16 * (BK * 2) + ch_off);
+            fb[i] = *reinterpret_cast<const half8_t *>(base + b_row_off + i * 16 * (BK * 2) + ch_off);
+        }
+        if (DB) {
+            lds_barrier();  // this stage's buffer is in registers: the issue waves may refill it
+        }
+        if (ks == 0) {
+            const uint32_t task = first + kc * stride;
+            const uint32_t item = task / ntiles;
+            c_nt = task - item * ntiles;
+            c_row0 = items[item * 4 + 1];
+            c_rows = items[item * 4 + 2];
+            live = wm * 64 < c_rows;
+            nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            if ((uint32_t)i < nlive) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (live && ks == steps - 1) {
+            uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
+            if (MODE == RMDA_GEMM_F16) {
+#pragma unroll
+                for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                    for (int v = 0; v < 4; v += 1) {
+                        const uint32_t rr = wm * 64 + i * 16 + rq + v;
+                        if (rr < c_rows) {
+#pragma unroll
+                            for (int j = 0; j < 4; j += 1) {
+                                const uint32_t col = c_nt * BN + wn * 64 + j * 16 + fr;
+                                O[(size_t)(c_row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
+                            }
+                        }
+                    }
+                }
+            } else {
+                const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
+                const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
+#pragma unroll
+                for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                    for (int v = 0; v < 4; v += 1) {
+                        const uint32_t rr = wm * 64 + i * 16 + rq + v;
+                        if (rr < c_rows) {
+#pragma unroll
+                            for (int j = 0; j < 2; j += 1) {
+                                const float gt = acc[i][j][v];
+                                const float up = acc[i][j + 2][v];
+                                const float h = gt / (1.0f + __expf(-gt)) * up;
+                                O[(size_t)(c_row0 + rr) * g.ldo + colbase + j * 16 + fr] = rmda_f2h(h);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        ks += 1;
+        if (ks == steps) {
+            ks = 0;
+            kc += 1;
+        }
+    }
+}
+
 // Packed slab image: for slab t (128 B rows) and K step ks, 16-byte unit
 // (n, p) holds B[slab_row(t, n)][ks*BK + (p ^ swz(n))*8 .. +8], at unit
 // index ((t * steps + ks) * 128 + n) * (BK/8) + p.
@@ -528,6 +795,14 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     // persistent: one workgroup per CU, a multiple of the 8 XCDs
     const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
     const dim3 grid(wgs);
+    if (c.spec != 0 && packed) {
+        if (c.spec == 5 || (c.spec == 6 && MODE == RMDA_GEMM_SWIGLU)) {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
+        } else {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
+        }
+        return hipGetLastError();
+    }
     if (c.stages == 4) {
         return launch_cfg<MODE, 256, 32, 4, 2>(s, a, grid, packed);
     }
@@ -540,12 +815,18 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
 }  // namespace
 
 // Variant 0 is the default: the fastest configuration measured on MI355X at
-// the benchmark shapes.  LDS per workgroup = STAGES * (192 + BN) * BK * 2.
+// the benchmark shapes (packed weights run the dedicated-issue kernel, with
+// the second per-stage barrier for gate_up only; HF-layout weights always run
+// gemm2_kernel).  The others are kept for measurement.  LDS per workgroup =
+// STAGES * (192 + BN) * BK * 2.
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     switch (variant) {
-    case 1: return {256, 32, 4, 0, 2};
-    case 2: return {256, 32, 5, 0, 0};
-    default: return {256, 32, 5, 0, 2};
+    case 1: return {256, 32, 5, 0, 2, 0};  // every MFMA wave issues its share of the loads
+    case 2: return {256, 32, 4, 0, 2, 0};  // the same with 4 stages
+    case 3: return {256, 32, 5, 0, 0, 0};  // the same without the non-temporal weight hint
+    case 4: return {256, 32, 5, 0, 2, 4};  // dedicated issue waves, one barrier per stage
+    case 5: return {256, 32, 5, 0, 2, 5};  // dedicated issue waves, two barriers per stage
+    default: return {256, 32, 5, 0, 2, 6};
     }
 }
 
