@@ -84,6 +84,25 @@ def test_layer_sampled(ctx, cfg_id):
     check_layer(ctx, configs.CONFIGS[cfg_id], seed=0, n_sample=48)
 
 
+@pytest.mark.parametrize("cfg", [
+    # one expert, shared expert on: every token in one group plus the dense group
+    dict(name="e1_shared", rows=37, d=256, experts=1, topk=1, inter=128, shared=128, skew=False),
+    # few experts, inter 128: gate_up N = 256 (one tile), down K = 128 (4 K steps)
+    dict(name="e6_i128", rows=77, d=256, experts=6, topk=2, inter=128, shared=0, skew=False),
+    # 130 columns: the router's fifth 32-column block holds 2 columns; top-k over 3 values per lane
+    dict(name="e130_k7", rows=129, d=768, experts=130, topk=7, inter=384, shared=0, skew=False),
+    # skewed routing at topk 1: hot experts get several 192-row work items
+    dict(name="skew_k1", rows=900, d=512, experts=24, topk=1, inter=256, shared=256, skew=True),
+    # maximum top-k, 512 experts, d not a multiple of 512 (1280 = 5 x 256: 10 sub-tiles per router chunk)
+    dict(name="e512_k16", rows=33, d=1280, experts=512, topk=16, inter=128, shared=0, skew=False),
+])
+def test_layer_more_shapes(ctx, cfg):
+    """Shapes away from the benchmark configurations, through both weight
+    layouts, against the oracle: routing bit-exact, output within tolerance,
+    packed bitwise equal to HF layout."""
+    check_layer(ctx, cfg, seed=3)
+
+
 def test_layer_other_seed_and_ragged(ctx):
     cfg = dict(configs.CONFIGS[1], rows=203, name="ragged")
     check_layer(ctx, cfg, seed=5)
