@@ -318,8 +318,10 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
  * gate_up GEMM -> grouped down GEMM -> (shared expert) -> combine, enqueued on
  * the context stream with no host synchronisation.
  * out[r] = sum_j wt[r,j] * FFN_{idx[r,j]}(x[r]) (+ sigmoid(g_r) * FFN_shared(x[r])).
- * Expert segments are packed without padding (tile 1); the permutation is
- * the stable order of rmda_moe_scatter.  Requires d % 256 == 0,
+ * Expert segments are padded to multiples of 16 rows (off[] is
+ * rmda_moe_scan with tile 16, so the activations between the two GEMMs are
+ * stored in whole 16-row blocks); the permutation is the stable order of
+ * rmda_moe_scatter over those offsets.  Requires d % 256 == 0,
  * inter % 128 == 0, shared == 0 or shared == inter, experts <= 512,
  * topk <= 16. */
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,

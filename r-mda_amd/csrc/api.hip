@@ -123,7 +123,7 @@ int prof_mark(rmda_moe_ctx_t *c, uint32_t st) {
 
 struct LayerPlan {
     size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, items, hp, ye, total;
-    uint32_t ps, npairs, nblocks, max_items, sh_rows, groups_rows;
+    uint32_t ps, npairs, nblocks, max_items, sh_rows, sh_row0, groups_rows;
 };
 
 int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
@@ -164,7 +164,11 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.nblocks = p.npairs == 0 ? 1 : (p.npairs + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
     p.sh_rows = s->shared > 0 ? T : 0;
     p.max_items = p.npairs / RMDA_GEMM2_BM + E + (p.sh_rows + RMDA_GEMM2_BM - 1) / RMDA_GEMM2_BM;
-    p.groups_rows = p.npairs + p.sh_rows;
+    // expert segments are padded to RMDA_HP_ROWS rows (at most 15 per expert),
+    // and the shared expert's rows follow at a multiple of RMDA_HP_ROWS
+    const uint32_t hpr = RMDA_HP_ROWS;
+    p.sh_row0 = (p.npairs + E * (hpr - 1) + hpr - 1) / hpr * hpr;
+    p.groups_rows = p.sh_row0 + (p.sh_rows + hpr - 1) / hpr * hpr;
     size_t o = 0;
     auto take = [&](size_t bytes) {
         size_t at = o;
@@ -176,7 +180,7 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.wt = take((size_t)p.npairs * 4);
     p.lrank = take((size_t)p.npairs * 4);
     p.slot = take((size_t)p.npairs * 4);
-    p.rowtok = take((size_t)(p.npairs + RMDA_ROWTOK_PAD) * 4);
+    p.rowtok = take((size_t)(p.sh_row0 + RMDA_ROWTOK_PAD) * 4);
     p.count = take((size_t)E * 4);
     p.off = take((size_t)E * 4);
     p.hist = take((size_t)p.nblocks * E * 4);
@@ -744,7 +748,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.idx = idx;
         ra.npairs = p.npairs;
         ra.experts = E;
-        ra.tile = 1;
+        ra.tile = RMDA_HP_ROWS;  // segments start at multiples of 16 rows (the hp block layout)
         ra.lrank = lrank;
         ra.hist = at<uint32_t>(ws, p.hist);
         ra.count = at<uint32_t>(ws, p.count);
@@ -754,7 +758,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.n_items = at<uint32_t>(ws, p.n_items);
         ra.bm = RMDA_GEMM2_BM;
         ra.shared_rows = p.sh_rows;
-        ra.shared_row0 = p.npairs;
+        ra.shared_row0 = p.sh_row0;
         rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
     }
     if (rc == RMDA_OK) {
@@ -775,7 +779,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     g.n_items = at<uint32_t>(ws, p.n_items);
     g.max_items = p.max_items;
     g.shared_group = shape->shared > 0 ? E : RMDA_NONE;
-    g.shared_row0 = p.npairs;
+    g.shared_row0 = p.sh_row0;
     g.sa = RMDA_NO_SLOT;
     g.sb = RMDA_NO_SLOT;
     // A4-A6 gate_up with SwiGLU epilogue -> hp16
@@ -820,7 +824,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     const rmda_hc_t hcp{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
-                       rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.npairs, shape->shared > 0, args->out,
+                       rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.sh_row0, shape->shared > 0, args->out,
                                              T, d, K, &hcp),
                        "layer combine");
     }

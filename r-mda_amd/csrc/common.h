@@ -263,6 +263,16 @@ struct rmda_gemm2_cfg_t {
 // rows of padding after the gathered-row index buffer (rowtok) that the
 // grouped GEMM's scalar index reads may touch
 #define RMDA_ROWTOK_PAD 256u
+// The fused layer's sorted rows: every expert segment (and the shared
+// expert's rows) starts at a multiple of RMDA_HP_ROWS, and the gate_up output
+// hp is stored in 1 KiB blocks of RMDA_HP_ROWS rows x 32 columns: element
+// (row R, column c) of an I-column hp at
+//   ((R / 16) * (I / 32) + c / 32) * 512 + (R % 16) * 32 + c % 32,
+// so the down GEMM loads a 16-row x 32-k tile of it as one contiguous KiB.
+#define RMDA_HP_ROWS 16u
+__host__ __device__ __forceinline__ size_t rmda_hp_index(uint32_t row, uint32_t col, uint32_t inter) {
+    return ((size_t)(row / 16) * (inter / 32) + col / 32) * 512 + (row % 16) * 32 + col % 32;
+}
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant);
 hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm2_cfg_t c, int packed);
 // Reorder `groups` row-major [n_w][k] matrices (fp16, or bf16 when bf16_in)

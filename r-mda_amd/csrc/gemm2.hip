@@ -159,6 +159,9 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t B_HI = (B_ALL + NWAVES - 1) / NWAVES;
     constexpr uint32_t B_LO = B_ALL / NWAVES;
     static_assert(A_PER >= 1 && AW % RPI == 0 && AW <= 16, "A rows per wave must fill DMA instructions");
+    // K step of an A load: the down GEMM's A (hp) is in 16-row x 32-column blocks
+    constexpr uint32_t A_STEP = MODE == RMDA_GEMM_F16 ? RMDA_HP_ROWS * BK : BK;
+    static_assert(MODE != RMDA_GEMM_F16 || (BK == 32 && RPI == RMDA_HP_ROWS), "hp block = one K step of one A instruction");
     static_assert(STAGES >= 2 && STAGES <= 6, "pipeline depth");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
 
@@ -247,7 +250,15 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
             } else {
                 arow = row0 + rr;
             }
-            a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+            if (MODE == RMDA_GEMM_F16) {
+                // hp is stored in 16-row x 32-column blocks: this instruction's 16 rows
+                // at one K step are one contiguous KiB (blocks past the item re-read its first)
+                const uint32_t blk = rbase + j * RPI;
+                a_src[j] = g.a + rmda_hp_index(row0 + (blk < rows ? blk : 0u), 0, g.lda) + lrow * 32 +
+                           (lch ^ swz<BK>(r)) * 8;
+            } else {
+                a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+            }
         }
 #pragma unroll
         for (uint32_t j = 0; j < B_HI; j += 1) {
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     // instruction q of this wave's stage: A rows first, then its B slices
     auto issue_one = [&](uint32_t q) __attribute__((always_inline)) {
         if (q < A_PER) {
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[q] + i_s * BK), (lds_void_t *)(ibase + a_dst[q]), 16,
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[q] + i_s * A_STEP), (lds_void_t *)(ibase + a_dst[q]), 16,
                                              0, 0);
         } else if (q - A_PER < n_b) {
             const uint32_t j = q - A_PER;
@@ -398,7 +409,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v];
                                 const float up = acc[i][j + 2][v];
                                 const float h = gt / (1.0f + __expf(-gt)) * up;
-                                O[(size_t)(c_row0 + rr) * g.ldo + colbase + j * 16 + fr] = rmda_f2h(h);
+                                O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
                             }
                         }
                     }
@@ -509,6 +520,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t AROWS = A_PER * RPI;     // A rows per issue wave
     static_assert(BM / RPI % NDW == 0 && BN / RPI % NDW == 0, "issue waves split a stage evenly");
     static_assert(AROWS <= 48, "gathered rows per issue wave");
+    constexpr uint32_t A_STEP = MODE == RMDA_GEMM_F16 ? RMDA_HP_ROWS * BK : BK;  // hp is in 16 x 32 blocks
     static_assert((NMW + NDW) * RMDA_WAVE <= 1024, "workgroup size");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
 
@@ -578,7 +590,13 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                 } else {
                     arow = row0 + rr;
                 }
-                a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+                if (MODE == RMDA_GEMM_F16) {
+                    const uint32_t blk = rbase + j * RPI;
+                    a_src[j] = g.a + rmda_hp_index(row0 + (blk < rows ? blk : 0u), 0, g.lda) + lrow * 32 +
+                               (lch ^ swz<BK>(r)) * 8;
+                } else {
+                    a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<BK>(r)) * 8;
+                }
             }
 #pragma unroll
             for (uint32_t j = 0; j < B_PER; j += 1) {
@@ -600,7 +618,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             uint8_t *base = smem + buf * STAGE_BYTES;
 #pragma unroll
             for (uint32_t j = 0; j < A_PER; j += 1) {
-                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + i_s * BK),
+                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + i_s * A_STEP),
                                                  (lds_void_t *)(base + (dw * AROWS + j * RPI) * (BK * 2)), 16, 0, 0);
             }
 #pragma unroll
@@ -724,7 +742,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v];
                                 const float up = acc[i][j + 2][v];
                                 const float h = gt / (1.0f + __expf(-gt)) * up;
-                                O[(size_t)(c_row0 + rr) * g.ldo + colbase + j * 16 + fr] = rmda_f2h(h);
+                                O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
                             }
                         }
                     }

@@ -50,7 +50,7 @@ def check_layer(ctx, cfg, seed, n_sample=None):
     sel = None
     if n_sample is not None and n_sample < T:
         sel = np.sort(np.random.default_rng(seed).choice(T, n_sample, replace=False)).astype(np.uint32)
-    ref = orc.layer(host, tile=1, rows_sel=sel)
+    ref = orc.layer(host, tile=16, rows_sel=sel)
     assert np.array_equal(views["proj"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
     assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
     assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
@@ -133,7 +133,7 @@ def test_layer_hyper_connection_epilogue(ctx, cfg_id, n_sample):
     sel = None
     if n_sample:
         sel = np.sort(np.random.default_rng(2).choice(T, n_sample, replace=False)).astype(np.uint32)
-    ref = orc.layer(host, tile=1, rows_sel=sel)
+    ref = orc.layer(host, tile=16, rows_sel=sel)
     rows = np.arange(T) if sel is None else sel.astype(np.int64)
     gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[rows, inj_off:inj_off + hc] / hc))
     want = h0.cpu().numpy()[rows].astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]
