@@ -252,6 +252,9 @@ hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 // numbers name the ones built (rmda_gemm2_variant; 0 = default).  Requires
 // n_w % 128 == 0 and k % bk == 0.
 #define RMDA_GEMM2_BM 192u
+// The rank kernel sorts the work list by rows in 16-row classes
+#define RMDA_ITEM_CLASSES 16u
+static_assert(RMDA_GEMM2_BM <= 16u * RMDA_ITEM_CLASSES, "work-item row classes");
 struct rmda_gemm2_cfg_t {
     uint32_t bn;
     uint32_t bk;

@@ -31,10 +31,10 @@
 //     once per launch, and keeping it out of the caches leaves them to the
 //     gathered activation rows and to the next kernel's inputs (gate_up
 //     176 vs 178 us, combine 14.7 vs 15.6 us at BASELINE config 3).
-//   * The grid is renumbered XCD-aware from the real work count read on the
-//     device: XCD x gets a contiguous range of (item, N tile) pairs, so the N
-//     tiles of one item (which share A rows) meet in one L2 and the 8 XCDs
-//     get equal shares whatever the routing.
+//   * Tasks are dealt XCD-aware from the real work count read on the device
+//     (task_sched_t): whole items go to XCDs, so the N tiles of one item
+//     (which share A rows) meet in one L2, and the list's row-count order
+//     lets alternating rounds even out every XCD's and workgroup's load.
 // MFMA: v_mfma_f32_16x16x32_f16, fp32 accumulate; 12 MFMA waves = 3 (M) x
 // 4 (N), 64 x 64 per wave.
 //
@@ -125,6 +125,49 @@ __device__ __forceinline__ void wait_stage(bool live, bool b_hi, uint32_t after)
     }
 }
 
+// Task schedule of a persistent launch: grid = 8 * S workgroups, workgroup b
+// on XCD b % 8.  The work list comes sorted by rows, largest first.
+//   * Item i goes to XCD snake(i / 8, i % 8, 8): the XCDs' shares balance,
+//     and the N tiles of one item (which share A rows) meet in one L2.
+//   * An XCD's tasks (its items in list order, N tiles innermost, so in
+//     falling cost) are dealt to its S workgroups round by round.  Rounds
+//     alternate direction so that pairs of rounds cancel; an odd number (>= 3)
+//     of full rounds starts with three rounds whose positions add up to
+//     3(S-1)/2 +- 1/2 for every workgroup.
+__device__ __forceinline__ uint32_t snake(uint32_t round, uint32_t pos, uint32_t width) {
+    return (round & 1u) != 0 ? width - 1u - pos : pos;
+}
+
+struct task_sched_t {
+    uint32_t xcd, wg, S, ntiles, full, ntask;
+    __device__ __forceinline__ task_sched_t(uint32_t n_items, uint32_t nt) {
+        xcd = blockIdx.x % 8u;
+        wg = blockIdx.x / 8u;
+        S = gridDim.x / 8u;
+        ntiles = nt;
+        const uint32_t rounds = n_items / 8u;
+        const uint32_t n_x = rounds + (snake(rounds, xcd, 8u) < n_items % 8u ? 1u : 0u);
+        const uint32_t total = n_x * nt;
+        full = total / S;
+        ntask = full + (pos(full) < total % S ? 1u : 0u);
+    }
+    // this workgroup's position in round q
+    __device__ __forceinline__ uint32_t pos(uint32_t q) const {
+        if (q < 3u && full >= 3u && (full & 1u) != 0 && (S & 1u) == 0) {
+            const uint32_t h = S / 2u;
+            return q == 0u ? wg : q == 1u ? (wg + h) % S : (wg < h ? S - 2u - 2u * wg : 2u * S - 1u - 2u * wg);
+        }
+        return snake(q, wg, S);
+    }
+    // work-list item of this workgroup's q-th task, and its N tile
+    __device__ __forceinline__ uint32_t item(uint32_t q, uint32_t &nt) const {
+        const uint32_t t = q * S + pos(q);
+        const uint32_t k = t / ntiles;
+        nt = t - k * ntiles;
+        return 8u * k + snake(k, xcd, 8u);
+    }
+};
+
 // Persistent workgroup: MB (=3) blocks of 64 rows x BN/64 (=4) column
 // blocks of 64, one wave each (12 waves).  Waves w and w + 4 share a SIMD, so
 // the four waves of a row block sit on four different SIMDs and any number of
@@ -171,21 +214,16 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     const uint32_t wm = w / NB;
     const uint32_t wn = w % NB;
 
-    // ---- this workgroup's tasks: XCD x owns a contiguous, equal share ----
+    // ---- this workgroup's tasks (task_sched_t) ----
     const_u32p items = (const_u32p)g.items;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
-    const uint32_t total = n_items * ntiles;
-    const uint32_t per = (total + 7) / 8;
-    const uint32_t xcd = blockIdx.x % 8;
-    const uint32_t stride = gridDim.x / 8;
-    const uint32_t first = xcd * per + blockIdx.x / 8;
-    const uint32_t last = min((xcd + 1) * per, total);
-    if (first >= last) {
+    const task_sched_t sched(n_items, ntiles);
+    const uint32_t ntask = sched.ntask;
+    if (ntask == 0) {
         return;
     }
-    const uint32_t ntask = (last - first + stride - 1) / stride;
     const uint32_t steps = g.k / BK;
     const uint32_t nstage = ntask * steps;
     const bool b_hi = w < B_ALL % NWAVES || B_ALL % NWAVES == 0;
@@ -209,9 +247,8 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
         b_dst[j] = A_BYTES + bi * RPI * (BK * 2);
     }
     auto setup = [&](uint32_t k) __attribute__((always_inline)) {
-        const uint32_t task = first + k * stride;
-        const uint32_t item = task / ntiles;
-        const uint32_t nt = task % ntiles;
+        uint32_t nt;
+        const uint32_t item = sched.item(k, nt);
         const uint32_t grp = items[item * 4 + 0];
         const uint32_t row0 = items[item * 4 + 1];
         const uint32_t rows = items[item * 4 + 2];
@@ -347,9 +384,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     // with the task bookkeeping; `between(q)` runs after group q (q < 3)
     auto compute_begin = [&]() __attribute__((always_inline)) {
         if (ks == 0) {
-            const uint32_t task = first + kc * stride;
-            const uint32_t item = task / ntiles;
-            c_nt = task - item * ntiles;
+            const uint32_t item = sched.item(kc, c_nt);
             c_row0 = items[item * 4 + 1];
             c_rows = items[item * 4 + 2];
             live = wm * 64 < c_rows;
@@ -528,21 +563,16 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
 
-    // ---- this workgroup's tasks: XCD x owns a contiguous, equal share ----
+    // ---- this workgroup's tasks (task_sched_t) ----
     const_u32p items = (const_u32p)g.items;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
-    const uint32_t total = n_items * ntiles;
-    const uint32_t per = (total + 7) / 8;
-    const uint32_t xcd = blockIdx.x % 8;
-    const uint32_t stride = gridDim.x / 8;
-    const uint32_t first = xcd * per + blockIdx.x / 8;
-    const uint32_t last = min((xcd + 1) * per, total);
-    if (first >= last) {
+    const task_sched_t sched(n_items, ntiles);
+    const uint32_t ntask = sched.ntask;
+    if (ntask == 0) {
         return;
     }
-    const uint32_t ntask = (last - first + stride - 1) / stride;
     const uint32_t steps = g.k / BK;
     const uint32_t nstage = ntask * steps;
 
@@ -554,9 +584,8 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
         const uint16_t *a_src[A_PER];
         const uint16_t *b_src[B_PER];
         auto setup = [&](uint32_t k) __attribute__((always_inline)) {
-            const uint32_t task = first + k * stride;
-            const uint32_t item = task / ntiles;
-            const uint32_t nt = task % ntiles;
+            uint32_t nt;
+            const uint32_t item = sched.item(k, nt);
             const uint32_t grp = items[item * 4 + 0];
             const uint32_t row0 = items[item * 4 + 1];
             const uint32_t rows = items[item * 4 + 2];
@@ -687,9 +716,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             lds_barrier();  // this stage's buffer is in registers: the issue waves may refill it
         }
         if (ks == 0) {
-            const uint32_t task = first + kc * stride;
-            const uint32_t item = task / ntiles;
-            c_nt = task - item * ntiles;
+            const uint32_t item = sched.item(kc, c_nt);
             c_row0 = items[item * 4 + 1];
             c_rows = items[item * 4 + 2];
             live = wm * 64 < c_rows;

@@ -101,6 +101,9 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     __shared__ uint32_t run[RMDA_MAX_EXPERTS];
     __shared__ uint32_t sbuf[NT / RMDA_WAVE];
     __shared__ uint32_t s_last;
+    __shared__ uint32_t cls_n[RMDA_ITEM_CLASSES];  // work-list items per 16-row class
+    __shared__ uint32_t cls_b[RMDA_ITEM_CLASSES];
+    __shared__ uint32_t sh_slot[2];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = tid / RMDA_WAVE;
@@ -248,37 +251,62 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     if (a.items == nullptr) {
         return;
     }
-    // grouped-GEMM work list: ceil(count/bm) items per expert, then the shared group
-    const uint32_t n0 = (c0 + a.bm - 1u) / a.bm;
-    const uint32_t n1 = (c1 + a.bm - 1u) / a.bm;
-    uint32_t routed = 0;
-    const uint32_t ib = block_exscan(n0 + n1, sbuf, &routed);
+    // Grouped-GEMM work list: ceil(count/bm) items per expert plus the shared
+    // group's, sorted by row count, largest first, in 16-row classes (the
+    // GEMMs deal the list out in that order to balance their workgroups).
+    // Each item takes a slot in its class with an LDS atomic, so the order
+    // inside a class varies from run to run; an item's result does not.
+    const uint32_t ncls = (a.bm + 15u) / 16u;
+    if (tid < RMDA_ITEM_CLASSES) {
+        cls_n[tid] = 0;
+    }
+    __syncthreads();
+    uint32_t nfull[2], last_cls[2], slot_full[2], slot_last[2];
+    for (uint32_t j = 0; j < 2; j += 1) {
+        const uint32_t c = j == 0 ? c0 : c1;
+        const uint32_t ni = (c + a.bm - 1u) / a.bm;
+        nfull[j] = ni > 0 ? ni - 1u : 0u;
+        last_cls[j] = ni > 0 ? (c - nfull[j] * a.bm + 15u) / 16u : 0u;
+        slot_full[j] = nfull[j] > 0 ? atomicAdd(&cls_n[ncls - 1u], nfull[j]) : 0u;
+        slot_last[j] = ni > 0 ? atomicAdd(&cls_n[last_cls[j] - 1u], 1u) : 0u;
+    }
+    const uint32_t ns = (a.shared_rows + a.bm - 1u) / a.bm;
+    if (tid == 0 && ns > 0) {
+        sh_slot[0] = ns > 1 ? atomicAdd(&cls_n[ncls - 1u], ns - 1u) : 0u;
+        sh_slot[1] = atomicAdd(&cls_n[(a.shared_rows - (ns - 1u) * a.bm + 15u) / 16u - 1u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t base = 0;
+        for (uint32_t c = ncls; c-- > 0;) {
+            cls_b[c] = base;
+            base += cls_n[c];
+        }
+        *a.n_items = base;
+    }
+    __syncthreads();
+    uint4 *items = reinterpret_cast<uint4 *>(a.items);
     for (uint32_t j = 0; j < 2; j += 1) {
         const uint32_t e = e0 + j;
         const uint32_t c = j == 0 ? c0 : c1;
-        const uint32_t ni = j == 0 ? n0 : n1;
-        const uint32_t first = j == 0 ? ib : ib + n0;
         const uint32_t o = j == 0 ? o0 : o1;
-        for (uint32_t i = 0; i < ni; i += 1) {
-            uint4 it;
-            it.x = e;
-            it.y = o + i * a.bm;
-            it.z = min(a.bm, c - i * a.bm);
-            it.w = 0;
-            reinterpret_cast<uint4 *>(a.items)[first + i] = it;
+        for (uint32_t i = 0; i < nfull[j]; i += 1) {
+            items[cls_b[ncls - 1u] + slot_full[j] + i] = make_uint4(e, o + i * a.bm, a.bm, 0u);
+        }
+        if (last_cls[j] > 0) {
+            const uint32_t i = nfull[j];
+            items[cls_b[last_cls[j] - 1u] + slot_last[j]] = make_uint4(e, o + i * a.bm, c - i * a.bm, 0u);
         }
     }
-    const uint32_t ns = (a.shared_rows + a.bm - 1u) / a.bm;
-    for (uint32_t i = tid; i < ns; i += NT) {
-        uint4 it;
-        it.x = E;
-        it.y = a.shared_row0 + i * a.bm;
-        it.z = min(a.bm, a.shared_rows - i * a.bm);
-        it.w = 0;
-        reinterpret_cast<uint4 *>(a.items)[routed + i] = it;
-    }
-    if (tid == 0) {
-        *a.n_items = routed + ns;
+    if (ns > 0) {
+        for (uint32_t i = tid; i + 1u < ns; i += NT) {
+            items[cls_b[ncls - 1u] + sh_slot[0] + i] = make_uint4(E, a.shared_row0 + i * a.bm, a.bm, 0u);
+        }
+        if (tid == 0) {
+            const uint32_t i = ns - 1u;
+            const uint32_t rows = a.shared_rows - i * a.bm;
+            items[cls_b[(rows + 15u) / 16u - 1u] + sh_slot[1]] = make_uint4(E, a.shared_row0 + i * a.bm, rows, 0u);
+        }
     }
 }
 

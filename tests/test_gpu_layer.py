@@ -30,6 +30,10 @@ def ctx():
 def run_layer(ctx, inp, packed=None):
     shape = inp["shape"]
     ws = inputs.workspace_for(shape)
+    # all-ones bytes are NaN as fp16: a GEMM task the schedule skipped would
+    # leave NaN activations that reach the output, not stale values of an
+    # earlier call
+    ws.fill_(255)
     out = torch.full((shape["rows"], shape["d"]), float("nan"), dtype=torch.float16, device="cuda")
     if packed is None:
         ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
@@ -125,6 +129,7 @@ def test_layer_hyper_connection_epilogue(ctx, cfg_id, n_sample):
     inj = torch.randn(T, inj_stride, device="cuda", generator=g) * 3
     h = h0.clone()
     ws = inputs.workspace_for(shape)
+    ws.fill_(255)  # NaN as fp16: nothing unwritten may reach h
     ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
               inp["w_sh_gate_up"], inp["w_sh_down"], None, ws, h=h, inj=inj, inj_stride=inj_stride,
               inj_off=inj_off, hc=hc)
