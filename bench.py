@@ -15,7 +15,10 @@ Prints ONE JSON line.  Besides the driver's fields it carries
   gemm          grouped-GEMM FLOP rate against the dense fp16 MFMA peak and
                 against the weight-streaming ceiling min(peak, BW * AI);
   cpu_baseline  the CPU oracle (a C restatement of the reference shaders)
-                timed on this host on a bounded sample of the same workload.
+                timed on this host on a bounded sample of the same workload;
+  decode        (config-3 runs) BASELINE configuration 2, T=128, timed the
+                same way: the weight-streaming regime's tokens/s and its two
+                GEMMs' HBM GB/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 """
@@ -54,6 +57,8 @@ def parse_args():
     ap.add_argument("--stages", action="store_true", help="print the stage table to stderr")
     ap.add_argument("--hf-layout", action="store_true",
                     help="stream the HF-layout weights instead of the packed ones")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-2 (T=128 decode) weight-streaming line added to the config-3 run")
     return ap.parse_args()
 
 
@@ -156,6 +161,52 @@ def measure_peaks(torch):
     torch.cuda.empty_cache()
     return {"hbm_copy_GB/s": round(copy_gbs, 1), "hbm_copy": "1 GiB device copy, 2*bytes/t",
             "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
+
+
+def measure_decode(ctx, torch, steps=100, warmup=50):
+    """BASELINE config 2 (T=128 decode), the weight-streaming regime: the
+    layer's rate and its two GEMMs' HBM rates, timed as the main line."""
+    from rmda_moe import api, configs, inputs
+
+    cfg = configs.CONFIGS[2]
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    shape = inp["shape"]
+    ws = inputs.workspace_for(shape)
+    out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
+    packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+
+    def step():
+        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed)
+
+    for _ in range(warmup):
+        step()
+    ctx.sync()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ctx.prof_begin()
+    for _ in range(steps):
+        step()
+    stage_ms, n_prof = ctx.prof_end()
+    counts = api.ws_views(shape, ws)["count"].cpu().numpy()
+    work = configs.algorithmic_work(cfg, touched=int((counts > 0).sum()))
+    res = {"workload": "decode: T=%d d=%d experts=%d top-%d inter=%d (BASELINE config 2)"
+                       % (shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"]),
+           "tokens/s": round(shape["rows"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 5), "steps": steps}
+    for k in ("gate_up", "down"):
+        us = 1000.0 * stage_ms[k] / max(n_prof, 1)
+        gbs = work[k + "_bytes"] / (us * 1e-6) / 1e9
+        res[k] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    del inp, ws, out, packed
+    torch.cuda.empty_cache()
+    return res
 
 
 def measure_upload(ctx, shape, torch):
@@ -324,6 +375,7 @@ def main():
 
     peaks = None if args.no_peaks else measure_peaks(torch)
     upload = measure_upload(ctx, shape, torch) if args.upload else None
+    decode = measure_decode(ctx, torch) if (args.config == 3 and not args.no_decode) else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -364,6 +416,7 @@ def main():
         "gemm": gemm,
         "hbm": hbm_small,
         "stages": stages,
+        "decode": decode,
         "cpu_baseline": cpu,
     }
     if cpu is not None:
