@@ -759,13 +759,19 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.bm = RMDA_GEMM2_BM;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.sh_row0;
+        if (p.nblocks == 1) {
+            // all pairs in one rank block: it writes the permutation too
+            ra.slot = slot;
+            ra.rowtok = rowtok;
+            ra.topk = K;
+        }
         rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_RANK + 1);
     }
     // A3 permutation (slots + row -> token map; x is gathered, not copied)
-    if (rc == RMDA_OK) {
+    if (rc == RMDA_OK && p.nblocks > 1) {
         rc = hip_check(ctx,
                        rmda_launch_permute(s, idx, lrank, at<uint32_t>(ws, p.hist), p.npairs, K, E, slot, rowtok,
                                            nullptr, nullptr, 0),
@@ -787,6 +793,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.mode = RMDA_GEMM_SWIGLU;
         g.a = args->x;
         g.rowtok = rowtok;
+        g.a_rows = T;
         g.lda = d;
         g.w = w_gu;
         g.w_shared = w_sgu;

@@ -205,6 +205,11 @@ struct rmda_rank_args_t {
     uint32_t bm;        // rows per work item
     uint32_t shared_rows; // rows of the shared-expert group (0 = none)
     uint32_t shared_row0; // sorted-row base of the shared group
+    // permutation written by the kernel itself when all pairs fit one rank
+    // block (npairs <= RMDA_RANK_BLOCK); ignored otherwise
+    uint32_t *slot;     // [npairs], or NULL
+    uint32_t *rowtok;   // [sorted rows] row -> token, or NULL
+    uint32_t topk;
 };
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);
 
@@ -225,6 +230,7 @@ struct rmda_gemm_args_t {
     int mode;
     const uint16_t *a;        // A base
     const uint32_t *rowtok;   // SWIGLU: sorted row -> token
+    uint32_t a_rows;          // SWIGLU: rows of A; a gathered token index is clamped below it
     uint32_t lda;             // elements
     const uint16_t *w;        // [groups][n_w][k]
     const uint16_t *w_shared; // group == shared_group uses this [n_w][k]

@@ -283,6 +283,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                         t = rl == c ? tok[c] : t;
                     }
                     arow = r < rows ? t : tok0;
+                    arow = arow < g.a_rows ? arow : 0u;  // a bad index reads a valid row, never out of bounds
                 }
             } else {
                 arow = row0 + rr;
@@ -615,6 +616,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                             t = lrow == c ? tok[c] : t;
                         }
                         arow = r < rows ? t : ((const_u32p)g.rowtok + row0)[0];
+                        arow = arow < g.a_rows ? arow : 0u;  // a bad index reads a valid row, never out of bounds
                     }
                 } else {
                     arow = row0 + rr;

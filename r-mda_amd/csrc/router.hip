@@ -163,8 +163,13 @@ typedef float rmda_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int MF_TOK = 16;  // tokens per 16x16 MFMA tile (A rows)
 constexpr int MF_TT = 2;    // token tiles per workgroup (32 tokens)
 constexpr int MF_TPW = 2;   // 16-column tiles per wave
-constexpr int MF_NCOL = 32; // columns per workgroup
-constexpr int MF_NW = 8 * MF_NCOL / (16 * MF_TPW);  // waves per workgroup: the 8 d chunks
+constexpr int MF_NCOL = 16 * MF_TPW;  // columns per workgroup
+constexpr int MF_NW = NQ;   // waves per workgroup: the 8 d chunks
+// Small tile for few tokens: 16 tokens x 16 columns, so that T = 128 still
+// spreads over 64 workgroups instead of 16
+constexpr int MF_TT_SMALL = 1;
+constexpr int MF_TPW_SMALL = 1;
+constexpr uint32_t MF_MIN_WGS = 128;  // below this many 32 x 32 workgroups, use the small tile
 constexpr int MF_KS = 16;   // k per sub-tile (4 MFMA steps)
 constexpr int MF_D = 3;     // sub-tiles a wave's loads run ahead of its MFMAs
 
@@ -181,8 +186,10 @@ __device__ __forceinline__ float h_hi(uint32_t v) { return rmda_h2f((uint16_t)(v
 // chunk, which is what the canonical order asks for; the chunk partials
 // are then added left to right as before.
 //
-// Workgroup = 32 tokens x 32 columns (2 x 2 output tiles); its 8 waves are
-// the 8 d chunks, each computing all four tiles of its chunk.  The matrix
+// Workgroup = 32 tokens x 32 columns (2 x 2 output tiles, TT = TPW = 2);
+// its 8 waves are the 8 d chunks, each computing all four tiles of its
+// chunk.  With few tokens (decode) the workgroup is 16 x 16 (TT = TPW = 1):
+// the same chunk chains, more workgroups.  The matrix
 // cores are not the limit (16x16x4 f32 issues at ~150 TF/s even from two
 // waves per SIMD): what a workgroup waits for is its operands, every one
 // of which misses L1 (weights are re-read by every token block, activations
@@ -207,16 +214,15 @@ __device__ __forceinline__ float h_hi(uint32_t v) { return rmda_h2f((uint16_t)(v
 // every logit of its tokens in LDS and routes them there, so the routing
 // needs no second launch.  Wider rows are routed by route_kernel: handing
 // logits between workgroups would need device-scope ordering across XCDs.
-template <bool W_PACKED, bool FUSE>
+template <bool W_PACKED, bool FUSE, int TT, int TPW>
 __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     const uint16_t *__restrict__ x16, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t cpad, uint32_t stride,
     uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, rmda_route_fuse_t fz) {
-    constexpr uint32_t NCOL = MF_NCOL;
-    constexpr int TPW = MF_TPW;
-    constexpr int TT = MF_TT;
+    constexpr uint32_t NCOL = 16 * TPW;
     constexpr int KS = MF_KS;
     constexpr uint32_t NW = MF_NW;
+    static_assert(NQ * NCOL / (16 * TPW) == NW, "one wave per d chunk and column slice");
     constexpr uint32_t NT = NW * RMDA_WAVE;
     constexpr uint32_t TOK = MF_TOK * TT;
     constexpr int SPS = KS / 4;   // MFMA steps per sub-tile
@@ -451,18 +457,33 @@ uint32_t rmda_router_cpad(uint32_t cols) { return (cols + RMDA_WAVE - 1) / RMDA_
 
 namespace {
 
+template <bool FUSE, int TT, int TPW>
+void launch_mf_tile(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
+                    const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
+                    uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
+    const dim3 grid((rows + MF_TOK * TT - 1) / (MF_TOK * TT), FUSE ? 1 : (cols + 16 * TPW - 1) / (16 * TPW));
+    const dim3 block(MF_NW * RMDA_WAVE);
+    if (w_packed) {
+        hipLaunchKernelGGL((router_mf_kernel<true, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz);
+    } else {
+        hipLaunchKernelGGL((router_mf_kernel<false, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz);
+    }
+}
+
 template <bool FUSE>
 void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
                const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
                uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
-    const dim3 grid((rows + MF_TOK * MF_TT - 1) / (MF_TOK * MF_TT), FUSE ? 1 : (cols + MF_NCOL - 1) / MF_NCOL);
-    const dim3 block(MF_NW * RMDA_WAVE);
-    if (w_packed) {
-        hipLaunchKernelGGL((router_mf_kernel<true, FUSE>), grid, block, 0, s, x16, w, bias, proj, rows, d, cols, cpad,
-                           stride, nbias, zero_words, n_zero, fz);
+    const uint32_t wgs = (rows + MF_TOK * MF_TT - 1) / (MF_TOK * MF_TT) * (FUSE ? 1u : (cols + MF_NCOL - 1) / MF_NCOL);
+    const bool small = wgs < MF_MIN_WGS && (!FUSE || cols <= 16u * MF_TPW_SMALL);
+    if (small) {
+        launch_mf_tile<FUSE, MF_TT_SMALL, MF_TPW_SMALL>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride,
+                                                        nbias, zero_words, n_zero, fz);
     } else {
-        hipLaunchKernelGGL((router_mf_kernel<false, FUSE>), grid, block, 0, s, x16, w, bias, proj, rows, d, cols, cpad,
-                           stride, nbias, zero_words, n_zero, fz);
+        launch_mf_tile<FUSE, MF_TT, MF_TPW>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride, nbias,
+                                            zero_words, n_zero, fz);
     }
 }
 

@@ -119,6 +119,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     // for the block instead of one per 256 pairs
     constexpr uint32_t ITS = RMDA_RANK_BLOCK / NT;
     uint32_t ev[ITS];
+    uint32_t lr[ITS];  // local ranks, kept for the single-block permutation
 #pragma unroll
     for (uint32_t it = 0; it < ITS; it += 1) {
         const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
@@ -143,6 +144,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             }
             r += __popcll(msk[w][e] & below);
             a.lrank[pr] = r;
+            lr[it] = r;
         }
         __syncthreads();
         for (uint32_t e2 = tid; e2 < E; e2 += NT) {
@@ -226,6 +228,32 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         }
         if (a.count != nullptr) {
             a.count[e0 + 1] = c1;
+        }
+    }
+    if (a.slot != nullptr && nb == 1) {
+        // One block holds every pair: it writes the permutation itself,
+        // slot = off[e] + local rank, and the row -> token map, so the
+        // separate permutation launch is not needed.  run[] (this block's
+        // counts, already stored) now holds the offsets.
+        __syncthreads();
+        if (own0) {
+            run[e0] = o0;
+        }
+        if (own1) {
+            run[e0 + 1] = o1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t it = 0; it < ITS; it += 1) {
+            const uint32_t pr = it * NT + tid;
+            if (pr < a.npairs) {
+                const uint32_t e = ev[it];
+                const uint32_t sl = e < E ? run[e] + lr[it] : RMDA_NONE;
+                a.slot[pr] = sl;
+                if (a.rowtok != nullptr && sl != RMDA_NONE) {
+                    a.rowtok[sl] = pr / a.topk;
+                }
+            }
         }
     }
     uint32_t acc0 = o0;

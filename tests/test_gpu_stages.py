@@ -45,8 +45,9 @@ def test_fill_matches_oracle_bitwise(ctx, n, stream, seed, std):
 # ---------------------------------------------------------------- router (A0)
 
 @pytest.mark.parametrize("rows,d,cols,stride,bias", [
-    (256, 512, 8, 8, False),       # config 1
-    (2048, 2048, 128, 128, False),  # config 3
+    (256, 512, 8, 8, False),       # config 1 (16 x 16 workgroup tile: few 32 x 32 workgroups)
+    (128, 2048, 128, 128, False),   # config 2, decode (16 x 16 tile)
+    (2048, 2048, 128, 128, False),  # config 3 (32 x 32 tile)
     (2048, 2048, 128, 130, True),   # config 4 (skew bias), padded stride
     (512, 2048, 513, 513, False),   # config 5 row subset: 512 experts + shared gate
     (37, 256, 70, 72, True),        # ragged tile edges
