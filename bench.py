@@ -18,7 +18,10 @@ Prints ONE JSON line.  Besides the driver's fields it carries
                 timed on this host on a bounded sample of the same workload;
   decode        (config-3 runs) BASELINE configuration 2, T=128, timed the
                 same way: the weight-streaming regime's tokens/s and its two
-                GEMMs' HBM GB/s.
+                GEMMs' HBM GB/s;
+  dropin        (config-3 runs) the reference-equivalent stage entry points
+                (route, scan, scatter into xp, combine) on the same inputs,
+                with their HBM GB/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 """
@@ -59,6 +62,8 @@ def parse_args():
                     help="stream the HF-layout weights instead of the packed ones")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the config-2 (T=128 decode) weight-streaming line added to the config-3 run")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip timing the reference-equivalent stage entry points (route, scan, scatter, combine)")
     return ap.parse_args()
 
 
@@ -205,6 +210,68 @@ def measure_decode(ctx, torch, steps=100, warmup=50):
         gbs = work[k + "_bytes"] / (us * 1e-6) / 1e9
         res[k] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     del inp, ws, out, packed
+    torch.cuda.empty_cache()
+    return res
+
+
+def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
+    """The reference-equivalent stage entry points on the same inputs, with
+    the reference's 128-row segments and fp32 expert outputs: route, scan,
+    scatter (materialises xp like shader/moe_scatter.comp), combine into four
+    hyper-connection streams and plain combine.  Bytes are the algorithmic
+    ones (padding and zero-fills excluded); route and scan are latency-bound."""
+    s = inp["shape"]
+    T, d, E, K = s["rows"], s["d"], s["experts"], s["topk"]
+    P, HC, HC_PAD = 128, 4, 8
+    mrows = (T * K + E * (P - 1) + P - 1) // P * P
+    dev = "cuda"
+    proj = torch.empty(T, E, dtype=torch.float32, device=dev)
+    ctx.router(T, d, E, E, 0, inp["x"], inp["w_router"], None, proj)
+    idx = torch.empty(T * K, dtype=torch.int32, device=dev)
+    wt = torch.empty(T * K, dtype=torch.float32, device=dev)
+    count = torch.empty(E, dtype=torch.int32, device=dev)
+    off = torch.empty(E, dtype=torch.int32, device=dev)
+    tiles = torch.empty(mrows // P, dtype=torch.int32, device=dev)
+    fill = torch.empty(E, dtype=torch.int32, device=dev)
+    slot = torch.empty(T * K, dtype=torch.int32, device=dev)
+    xp = torch.zeros(mrows, d, dtype=torch.float16, device=dev)
+    y = torch.randn(mrows, d, dtype=torch.float32, device=dev)
+    h = torch.zeros(T, HC, d, dtype=torch.float32, device=dev)
+    inj = torch.randn(T, HC_PAD, dtype=torch.float32, device=dev)
+    out = torch.empty(T, d, dtype=torch.float16, device=dev)
+    fields = (T, d, K, E, E, HC_PAD, 0, HC)
+    ctx.scatter_experts(E)
+    stages = [
+        ("route", lambda: ctx.route(T, E, K, E, proj, idx, wt, count), T * E * 4 + T * K * 8 + E * 4),
+        ("scan", lambda: ctx.scan(E, P, count, off, tiles, mrows // P), 0),
+        ("scatter", lambda: ctx.scatter(T, K, d // 8, idx, off, fill, inp["x"], xp, slot),
+         T * d * 2 + T * K * d * 2 + T * K * 8),
+        ("combine_hc", lambda: ctx.combine(fields, wt, slot, y, proj, None, inj, h),
+         T * K * d * 4 + T * K * 8 + T * HC * d * 4 * 2 + T * HC_PAD * 4),
+        ("combine_plain", lambda: ctx.combine_plain(fields, wt, slot, y, proj, None, out),
+         T * K * d * 4 + T * K * 8 + T * d * 2),
+    ]
+    res = {"workload": "BASELINE config 3 inputs, reference segments P=%d (mrows %d), fp32 expert outputs" % (P, mrows)}
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for name, fn, nbytes in stages:
+        for _ in range(warmup):
+            fn()
+        ctx.sync()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / iters
+        res[name] = {"us": round(us, 2)}
+        if nbytes:
+            gbs = nbytes / (us * 1e-6) / 1e9
+            res[name].update({"bytes": nbytes, "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    sc_b = res["scatter"]["bytes"] + res["combine_hc"]["bytes"]
+    sc_us = res["scatter"]["us"] + res["combine_hc"]["us"]
+    res["scatter+combine_hc_GB/s"] = round(sc_b / (sc_us * 1e-6) / 1e9, 1)
+    del proj, idx, wt, count, off, tiles, fill, slot, xp, y, h, inj, out
     torch.cuda.empty_cache()
     return res
 
@@ -376,6 +443,7 @@ def main():
     peaks = None if args.no_peaks else measure_peaks(torch)
     upload = measure_upload(ctx, shape, torch) if args.upload else None
     decode = measure_decode(ctx, torch) if (args.config == 3 and not args.no_decode) else None
+    dropin = measure_dropins(ctx, torch, inp) if (args.config == 3 and not args.no_dropin) else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -417,6 +485,7 @@ def main():
         "hbm": hbm_small,
         "stages": stages,
         "decode": decode,
+        "dropin": dropin,
         "cpu_baseline": cpu,
     }
     if cpu is not None:

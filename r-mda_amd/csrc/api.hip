@@ -410,11 +410,33 @@ int rmda_moe_route(rmda_moe_ctx_t *ctx, const rmda_pc_moe_route_t *pc, const flo
     if (pc->stride < pc->experts) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_route: stride=%u < experts=%u", pc->stride, pc->experts);
     }
-    rc = hip_check(ctx, rmda_launch_zero(ctx->stream, count, pc->experts, 0), "zero count");
-    if (rc == RMDA_OK) {
-        rc = hip_check(ctx, rmda_launch_route(ctx->stream, proj, idx, wt, count, pc->rows, pc->experts, pc->topk,
+    const uint64_t npairs = (uint64_t)pc->rows * pc->topk;
+    if (npairs <= RMDA_CTX_MAX_PAIRS) {
+        // top-k without atomics, then the counts from rank_kernel's per-block
+        // histograms (16 K atomic adds onto E counters contend: 31 us against
+        // about 12 us at config 3)
+        rc = hip_check(ctx, rmda_launch_route(ctx->stream, proj, idx, wt, nullptr, pc->rows, pc->experts, pc->topk,
                                               pc->stride),
                        "route");
+        if (rc == RMDA_OK) {
+            rmda_rank_args_t ra{};
+            ra.idx = idx;
+            ra.npairs = (uint32_t)npairs;
+            ra.experts = pc->experts;
+            ra.tile = 1;
+            ra.lrank = ctx->lrank;
+            ra.hist = ctx->hist;
+            ra.count = count;
+            ra.done = ctx->done;
+            rc = hip_check(ctx, rmda_launch_rank(ctx->stream, &ra), "route counts");
+        }
+    } else {
+        rc = hip_check(ctx, rmda_launch_zero(ctx->stream, count, pc->experts, 0), "zero count");
+        if (rc == RMDA_OK) {
+            rc = hip_check(ctx, rmda_launch_route(ctx->stream, proj, idx, wt, count, pc->rows, pc->experts, pc->topk,
+                                                  pc->stride),
+                           "route");
+        }
     }
     if (rc == RMDA_OK) {
         ctx->scatter_experts = pc->experts;

@@ -5,6 +5,9 @@
 // sigmoid(inj / hc)), plus a plain fp16 output mode.  One thread per output
 // element, like the reference.
 //
+// combine32_kernel is its bandwidth version for the drop-in entry points
+// (d % 4 == 0; combine_ref_kernel remains for other d).
+//
 // combine16_kernel is the fused layer's version: fp16 expert rows, fp16
 // output and/or the hyper-connection streams, one workgroup per token.  The token's topk (slot, weight) pairs are
 // read once into LDS; each thread then handles 8 consecutive columns with
@@ -50,6 +53,81 @@ __global__ __launch_bounds__(256) void combine_ref_kernel(rmda_pc_moe_combine_t 
     for (uint32_t s = 0; s < pc.hc; s += 1) {
         const float gte = sigmoidf(inj[(size_t)r * pc.inj_stride + pc.inj_off + s] / (float)pc.hc);
         h[(size_t)r * pc.hc * pc.d + (size_t)s * pc.d + c] += acc * 2.0f * gte;
+    }
+}
+
+// The drop-in combine (rmda_moe_combine / _plain) at bandwidth: the same
+// arithmetic as combine_ref_kernel per element (fp32 y rows, acc += wt*y in
+// j order, then the shared term, then the hc streams or the fp16 output), but
+// one workgroup per token: the token's slots, weights and stream gates are
+// read once into LDS and each thread moves 4 consecutive columns with 16-byte
+// loads and stores.  Needs d % 4 == 0.
+template <bool HC>
+__global__ __launch_bounds__(256) void combine32_kernel(rmda_pc_moe_combine_t pc,
+                                                        const float *__restrict__ wt,
+                                                        const uint32_t *__restrict__ slot,
+                                                        const float *__restrict__ y,
+                                                        const float *__restrict__ proj,
+                                                        const float *__restrict__ sh,
+                                                        const float *__restrict__ inj,
+                                                        float *__restrict__ h,
+                                                        uint16_t *__restrict__ out) {
+    __shared__ uint32_t s_slot[RMDA_MAX_TOPK];
+    __shared__ float s_wt[RMDA_MAX_TOPK];
+    __shared__ float s_g[RMDA_MAX_HC];
+    __shared__ float s_sg;
+    const uint32_t r = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    if (tid < pc.topk) {
+        s_slot[tid] = slot[(size_t)r * pc.topk + tid];
+        s_wt[tid] = wt[(size_t)r * pc.topk + tid];
+    }
+    if (tid == 0 && sh != nullptr) {
+        s_sg = sigmoidf(proj[(size_t)r * pc.pstride + pc.sg_off]);
+    }
+    if (HC && tid < pc.hc) {
+        s_g[tid] = sigmoidf(inj[(size_t)r * pc.inj_stride + pc.inj_off + tid] / (float)pc.hc);
+    }
+    __syncthreads();
+    const uint32_t d4 = pc.d / 4;
+    for (uint32_t c = tid; c < d4; c += 256) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t j = 0; j < pc.topk; j += 1) {
+            const uint32_t s = s_slot[j];
+            if (s == RMDA_NONE) {
+                continue;
+            }
+            const float wj = s_wt[j];
+            const float4 v = reinterpret_cast<const float4 *>(y + (size_t)s * pc.d)[c];
+            acc.x += wj * v.x;
+            acc.y += wj * v.y;
+            acc.z += wj * v.z;
+            acc.w += wj * v.w;
+        }
+        if (sh != nullptr) {
+            const float4 v = reinterpret_cast<const float4 *>(sh + (size_t)r * pc.d)[c];
+            acc.x += s_sg * v.x;
+            acc.y += s_sg * v.y;
+            acc.z += s_sg * v.z;
+            acc.w += s_sg * v.w;
+        }
+        if (!HC) {
+            uint2 o;
+            o.x = (uint32_t)rmda_f2h(acc.x) | ((uint32_t)rmda_f2h(acc.y) << 16);
+            o.y = (uint32_t)rmda_f2h(acc.z) | ((uint32_t)rmda_f2h(acc.w) << 16);
+            reinterpret_cast<uint2 *>(out + (size_t)r * pc.d)[c] = o;
+        } else {
+            for (uint32_t st = 0; st < pc.hc; st += 1) {
+                float4 *hp = reinterpret_cast<float4 *>(h + ((size_t)r * pc.hc + st) * pc.d) + c;
+                const float g = s_g[st];
+                float4 a = *hp;
+                a.x += acc.x * 2.0f * g;
+                a.y += acc.y * 2.0f * g;
+                a.z += acc.z * 2.0f * g;
+                a.w += acc.w * 2.0f * g;
+                *hp = a;
+            }
+        }
     }
 }
 
@@ -148,6 +226,16 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
     const uint64_t n = (uint64_t)pc->rows * pc->d;
     if (n == 0) {
         return hipSuccess;
+    }
+    if (pc->d % 4 == 0 && pc->topk <= RMDA_MAX_TOPK && pc->hc <= RMDA_MAX_HC) {
+        if (out != nullptr) {
+            hipLaunchKernelGGL(combine32_kernel<false>, dim3(pc->rows), dim3(256), 0, s, *pc, wt, slot, y, proj, sh,
+                               inj, h, out);
+        } else {
+            hipLaunchKernelGGL(combine32_kernel<true>, dim3(pc->rows), dim3(256), 0, s, *pc, wt, slot, y, proj, sh,
+                               inj, h, out);
+        }
+        return hipGetLastError();
     }
     hipLaunchKernelGGL(combine_ref_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, *pc, wt, slot,
                        y, proj, sh, inj, h, out);

@@ -285,10 +285,11 @@ def test_moe_mm_vs_oracle(ctx, m, n, k, E, scaled):
 
 # ---------------------------------------------------------------- combine (A9) and helpers
 
+@pytest.mark.parametrize("d", [256, 2048, 258])  # 258: d % 4 != 0 takes the per-element kernel
 @pytest.mark.parametrize("shared,hc", [(False, 4), (True, 4), (True, 0)])
-def test_combine_vs_oracle(ctx, shared, hc):
+def test_combine_vs_oracle(ctx, shared, hc, d):
     r = rng(17)
-    rows, d, topk, E = 300, 256, 8, 64
+    rows, topk, E = 300, 8, 64
     nrows = rows * topk + 50
     p = r.standard_normal((rows, E + 3)).astype(np.float32)
     idx, wt, cnt = orc.route(p, E, topk)
