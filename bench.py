@@ -268,6 +268,33 @@ def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
         if nbytes:
             gbs = nbytes / (us * 1e-6) / 1e9
             res[name].update({"bytes": nbytes, "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)})
+    # the reference's grouped GEMM (matmul_f16_moe): 128-row tiles of xp,
+    # HF [E][n][k] weights, fp32 C; gate_up then down on a fp16 stand-in for hp16
+    I = s["inter"]
+    NO_SLOT = 0xFFFFFFFF
+    g32 = torch.empty(mrows, 2 * I, dtype=torch.float32, device=dev)
+    hp16 = torch.randn(mrows, I, dtype=torch.float16, device=dev)
+    ye32 = torch.empty(mrows, d, dtype=torch.float32, device=dev)
+    mm = [
+        ("mm_gate_up", lambda: ctx.mm(mrows, 2 * I, d, NO_SLOT, NO_SLOT, xp, inp["w_gate_up"], g32, None, tiles),
+         4 * T * K * d * I, E * 2 * I * d * 2 + T * K * d * 2 + T * K * 2 * I * 4),
+        ("mm_down", lambda: ctx.mm(mrows, d, I, NO_SLOT, NO_SLOT, hp16, inp["w_down"], ye32, None, tiles),
+         2 * T * K * d * I, E * d * I * 2 + T * K * I * 2 + T * K * d * 4),
+    ]
+    for name, fn, flops, nbytes in mm:
+        for _ in range(3):
+            fn()
+        ctx.sync()
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / 10
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 2), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), "bytes": nbytes,
+                     "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    del g32, hp16, ye32
     sc_b = res["scatter"]["bytes"] + res["combine_hc"]["bytes"]
     sc_us = res["scatter"]["us"] + res["combine_hc"]["us"]
     res["scatter+combine_hc_GB/s"] = round(sc_b / (sc_us * 1e-6) / 1e9, 1)
