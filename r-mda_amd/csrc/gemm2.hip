@@ -786,6 +786,272 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     }
 }
 
+// gate_up with the gathered activation rows in a ring of their own, two K
+// steps per slot.  gemm3_kernel fetches each gathered row as one 64-byte
+// piece per K step; here every row is one 128-byte line per pair of K steps
+// (8 rows per DMA instruction), so the activation rows need half the load
+// requests.  Weights keep their STAGES-deep ring of one K step each.
+//   * The six activation instructions of a pair (per issue wave) are issued
+//     with the pair's first stage, into slot (pair % 3).  The slot's previous
+//     pair was last read five stages earlier, before the barrier that lets
+//     this stage be issued, so three slots cover the five stages in flight.
+//   * Even stages carry 6 + 4 loads per issue wave, odd ones 4: any four
+//     consecutive stages hold 28, so the waits stay compile-time constants.
+//   * LDS: 5 x 16 KiB of weights + 3 x 24 KiB of activations = 152 KiB.  An
+//     activation row is 128 bytes; chunk c of row r sits at c ^ ((r>>1)&7),
+//     so each 16-lane fragment read touches 16 distinct bank groups.
+// Needs k % 64 == 0 (pairs never straddle a task).
+template <int STAGES, int BPOL, int NDW>
+__global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
+    constexpr uint32_t BN = 256;
+    constexpr uint32_t BK = 32;
+    constexpr uint32_t MB = BM / 64;
+    constexpr uint32_t NB = BN / 64;
+    constexpr uint32_t NMW = MB * NB;             // 12 MFMA waves
+    constexpr uint32_t CH = BK / 8;               // 16-byte chunks per weight row
+    constexpr uint32_t RPI = 64 / CH;             // weight rows per DMA instruction
+    constexpr uint32_t B_BYTES = BN * BK * 2;     // one weight stage
+    constexpr uint32_t B_PER = BN / RPI / NDW;    // weight instructions per issue wave per stage
+    constexpr uint32_t AK = 2 * BK;               // activation slot: two K steps per row
+    constexpr uint32_t ACH = AK / 8;              // 16-byte chunks per activation row
+    constexpr uint32_t ARPI = 64 / ACH;           // activation rows per DMA instruction
+    constexpr uint32_t A_SLOT = BM * AK * 2;
+    constexpr uint32_t A_SLOTS = 3;
+    constexpr uint32_t A_PER = BM / ARPI / NDW;   // activation instructions per issue wave per pair
+    constexpr uint32_t AROWS = A_PER * ARPI;      // activation rows per issue wave
+    constexpr uint32_t AHEAD = STAGES;            // two barriers per stage: every buffer in flight
+    constexpr uint32_t LE = A_PER + B_PER;        // loads of an even (pair-opening) stage
+    constexpr uint32_t LO = B_PER;                // loads of an odd stage
+    static_assert(STAGES == 5 && 2 * A_SLOTS == AHEAD + 1, "slot reuse argument above");
+    static_assert(BM % (ARPI * NDW) == 0 && BN / RPI % NDW == 0, "issue waves split a stage evenly");
+    static_assert(2 * (LE + LO) < 64, "vmcnt range");
+    static_assert((NMW + NDW) * RMDA_WAVE <= 1024, "workgroup size");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * B_BYTES + A_SLOTS * A_SLOT];
+    uint8_t *const bring = smem;
+    uint8_t *const aring = smem + STAGES * B_BYTES;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % RMDA_WAVE;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
+
+    const_u32p items = (const_u32p)g.items;
+    const uint32_t n_slabs = g.n_w / SLAB;
+    const uint32_t ntiles = n_slabs / (BN / SLAB);
+    const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
+    const task_sched_t sched(n_items, ntiles);
+    const uint32_t ntask = sched.ntask;
+    if (ntask == 0) {
+        return;
+    }
+    const uint32_t steps = g.k / BK;
+    const uint32_t nstage = ntask * steps;
+
+    if (w >= NMW) {
+        // ================= issue waves =================
+        const uint32_t dw = w - NMW;
+        const uint32_t lrow = lane / ACH;  // activation row within one instruction
+        const uint32_t lch = lane % ACH;   // its LDS chunk position
+        const uint16_t *a_src[A_PER];
+        const uint16_t *b_src[B_PER];
+        auto setup = [&](uint32_t k) __attribute__((always_inline)) {
+            uint32_t nt;
+            const uint32_t item = sched.item(k, nt);
+            const uint32_t grp = items[item * 4 + 0];
+            const uint32_t row0 = items[item * 4 + 1];
+            const uint32_t rows = items[item * 4 + 2];
+            const bool is_shared = grp == g.shared_group;
+            const uint16_t *wg = is_shared ? g.w_shared : g.w + (size_t)grp * g.n_w * g.k;
+            const uint32_t rbase = dw * AROWS;
+#pragma unroll
+            for (uint32_t j = 0; j < A_PER; j += 1) {
+                const uint32_t r = rbase + j * ARPI + lrow;
+                uint32_t arow;
+                if (is_shared) {
+                    arow = row0 + (r < rows ? r : 0u) - g.shared_row0;
+                } else {
+                    const const_u32p rt = (const_u32p)g.rowtok + row0 + rbase + j * ARPI;
+                    uint32_t tok[ARPI];
+#pragma unroll
+                    for (uint32_t c = 0; c < ARPI; c += 1) {
+                        tok[c] = rt[c];
+                    }
+                    uint32_t t = tok[0];
+#pragma unroll
+                    for (uint32_t c = 1; c < ARPI; c += 1) {
+                        t = lrow == c ? tok[c] : t;
+                    }
+                    arow = r < rows ? t : ((const_u32p)g.rowtok + row0)[0];
+                    arow = arow < g.a_rows ? arow : 0u;  // a bad index reads a valid row, never out of bounds
+                }
+                a_src[j] = g.a + (size_t)arow * g.lda + (lch ^ swz<AK>(r)) * 8;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                const uint32_t nbase = (dw * B_PER + j) * RPI;
+                const uint32_t slab = nt * (BN / SLAB) + nbase / SLAB;
+                const uint32_t nin = nbase % SLAB;
+                b_src[j] = wg + (size_t)slab * steps * (SLAB * BK) + nin * BK + lane * 8;
+            }
+        };
+        uint32_t i_task = 0;
+        uint32_t i_s = 0;
+        uint32_t aslot = 0;
+        setup(0);
+        auto issue = [&](uint32_t buf) __attribute__((always_inline)) {
+            if (i_s == steps) {
+                i_task += 1;
+                i_s = 0;
+                setup(i_task);
+            }
+            // activation rows first (weights first measured slower at config 3)
+            if ((i_s & 1u) == 0) {
+                uint8_t *abase = aring + aslot * A_SLOT;
+                aslot = aslot + 1 == A_SLOTS ? 0 : aslot + 1;
+#pragma unroll
+                for (uint32_t j = 0; j < A_PER; j += 1) {
+                    __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + (i_s / 2) * AK),
+                                                     (lds_void_t *)(abase + (dw * AROWS + j * ARPI) * (AK * 2)),
+                                                     16, 0, 0);
+                }
+            }
+            uint8_t *bbase = bring + buf * B_BYTES;
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                __builtin_amdgcn_global_load_lds((const void *)(b_src[j] + (size_t)i_s * (SLAB * BK)),
+                                                 (lds_void_t *)(bbase + (dw * B_PER + j) * RPI * (BK * 2)), 16,
+                                                 0, BPOL);
+            }
+            i_s += 1;
+        };
+#pragma unroll
+        for (uint32_t st = 0; st < AHEAD; st += 1) {
+            if (st < nstage) {
+                issue(st);
+            }
+        }
+        uint32_t ibuf = AHEAD % STAGES;
+        for (uint32_t gs = 0; gs < nstage; gs += 1) {
+            // stage gs has landed once only the loads of the `later` stages
+            // issued after it remain; their count depends on gs's parity
+            const uint32_t later = min(nstage - 1 - gs, AHEAD - 1);
+            const bool odd = (gs & 1u) != 0;
+            switch (later) {
+            case 0: wait_vm<0>(); break;
+            case 1:
+                if (odd) {
+                    wait_vm<LE>();
+                } else {
+                    wait_vm<LO>();
+                }
+                break;
+            case 2: wait_vm<LE + LO>(); break;
+            case 3:
+                if (odd) {
+                    wait_vm<LE + LO + LE>();
+                } else {
+                    wait_vm<LO + LE + LO>();
+                }
+                break;
+            default: wait_vm<2 * (LE + LO)>(); break;
+            }
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_s_barrier();
+            if (gs + AHEAD < nstage) {
+                issue(ibuf);
+                ibuf = ibuf + 1 == STAGES ? 0 : ibuf + 1;
+            }
+        }
+        return;
+    }
+
+    // ================= MFMA waves =================
+    const uint32_t wm = w / NB;
+    const uint32_t wn = w % NB;
+    const uint32_t fr = lane % 16;
+    const uint32_t fq = lane / 16;
+    // activation fragment of K step half h: chunk 4h + fq of row wm*64 + 16i + fr
+    const uint32_t a_row = (wm * 64 + fr) * (AK * 2);
+    const uint32_t a_off0 = a_row + ((0u + fq) ^ swz<AK>(fr)) * 16;
+    const uint32_t a_off1 = a_row + ((4u + fq) ^ swz<AK>(fr)) * 16;
+    const uint32_t b_off = (wn * 64 + fr) * (BK * 2) + (fq ^ swz<BK>(fr)) * 16;
+    const uint32_t rq = 4 * fq;
+    floatx4_t acc[4][4];
+    uint32_t c_row0 = 0;
+    uint32_t c_rows = 0;
+    uint32_t c_nt = 0;
+    uint32_t kc = 0;
+    uint32_t ks = 0;
+    bool live = false;
+    uint32_t nlive = 0;
+    uint32_t cbuf = 0;
+    uint32_t abuf = 0;
+    for (uint32_t gs = 0; gs < nstage; gs += 1) {
+        lds_barrier();
+        const uint8_t *bb = bring + cbuf * B_BYTES + b_off;
+        const uint8_t *ab = aring + abuf * A_SLOT + ((gs & 1u) != 0 ? a_off1 : a_off0);
+        cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
+        if ((gs & 1u) != 0) {
+            abuf = abuf + 1 == A_SLOTS ? 0 : abuf + 1;
+        }
+        half8_t fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            fa[i] = *reinterpret_cast<const half8_t *>(ab + i * 16 * (AK * 2));
+            fb[i] = *reinterpret_cast<const half8_t *>(bb + i * 16 * (BK * 2));
+        }
+        lds_barrier();  // both buffers are in registers: the issue waves may refill them
+        if (ks == 0) {
+            const uint32_t item = sched.item(kc, c_nt);
+            c_row0 = items[item * 4 + 1];
+            c_rows = items[item * 4 + 2];
+            live = wm * 64 < c_rows;
+            nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            if ((uint32_t)i < nlive) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (live && ks == steps - 1) {
+            uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
+            const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
+            const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int v = 0; v < 4; v += 1) {
+                    const uint32_t rr = wm * 64 + i * 16 + rq + v;
+                    if (rr < c_rows) {
+#pragma unroll
+                        for (int j = 0; j < 2; j += 1) {
+                            const float gt = acc[i][j][v];
+                            const float up = acc[i][j + 2][v];
+                            const float h = gt / (1.0f + __expf(-gt)) * up;
+                            O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
+                        }
+                    }
+                }
+            }
+        }
+        ks += 1;
+        if (ks == steps) {
+            ks = 0;
+            kc += 1;
+        }
+    }
+}
+
 // Packed slab image: for slab t (128 B rows) and K step ks, 16-byte unit
 // (n, p) holds B[slab_row(t, n)][ks*BK + (p ^ swz(n))*8 .. +8], at unit
 // index ((t * steps + ks) * 128 + n) * (BK/8) + p.
@@ -843,7 +1109,11 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
     const dim3 grid(wgs);
     if (c.spec != 0 && packed) {
-        if (c.spec == 5 || (c.spec == 6 && MODE == RMDA_GEMM_SWIGLU)) {
+        if (c.spec == 7 && MODE == RMDA_GEMM_SWIGLU && a->k % 64 == 0) {
+            hipLaunchKernelGGL((gemm4_kernel<5, 2, 4>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
+            return hipGetLastError();
+        }
+        if (c.spec == 5 || ((c.spec == 6 || c.spec == 7) && MODE == RMDA_GEMM_SWIGLU)) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
         } else {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
@@ -863,8 +1133,10 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
 
 // Variant 0 is the default: the fastest configuration measured on MI355X at
 // the benchmark shapes (packed weights run the dedicated-issue kernel, with
-// the second per-stage barrier for gate_up only; HF-layout weights always run
-// gemm2_kernel).  The others are kept for measurement.  LDS per workgroup =
+// the second per-stage barrier for gate_up only, and the layer switches
+// gate_up to the activation-ring kernel when experts average 32 rows or
+// more; HF-layout weights always run gemm2_kernel).  The others are kept for
+// measurement.  LDS per workgroup =
 // STAGES * (192 + BN) * BK * 2.
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     switch (variant) {
@@ -873,6 +1145,7 @@ rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     case 3: return {256, 32, 5, 0, 0, 0};  // the same without the non-temporal weight hint
     case 4: return {256, 32, 5, 0, 2, 4};  // dedicated issue waves, one barrier per stage
     case 5: return {256, 32, 5, 0, 2, 5};  // dedicated issue waves, two barriers per stage
+    case 7: return {256, 32, 5, 0, 2, 7};  // gate_up with its activation rows in a two-K-step ring
     default: return {256, 32, 5, 0, 2, 6};
     }
 }
