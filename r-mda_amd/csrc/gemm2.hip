@@ -38,10 +38,14 @@
 // MFMA: v_mfma_f32_16x16x32_f16, fp32 accumulate; 12 MFMA waves = 3 (M) x
 // 4 (N), 64 x 64 per wave.
 //
-// Two kernels share this design:
+// Three kernels share this design:
 //   * gemm2_kernel: every MFMA wave also issues its share of each stage's
 //     DMA, between its MFMA groups (HF-layout weights, and measurement
 //     variants for packed ones).
+//   * gemm4_kernel (gate_up when experts average 32 rows or more): as
+//     gemm3_kernel below, with the gathered activation rows in a ring of
+//     their own, two K steps per slot, so each row is one 128-byte line per
+//     pair of K steps.
 //   * gemm3_kernel (packed weights, the default): four more waves issue all
 //     of the DMA and nothing else, so a stage's loads leave right after the
 //     stage barrier instead of queueing behind MFMAs; for gate_up a second
