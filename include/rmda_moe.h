@@ -455,6 +455,92 @@ int rmda_moe_fill_normal_f16(rmda_moe_ctx_t *ctx, uint16_t *dst, size_t n,
 int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n,
                              uint64_t stream, uint64_t seed, float std);
 
+/* ---- the qwen.c MoE recording (src/qwen.c:770-907) over the stage entry
+ * points ----
+ * The reference records a layer's MoE with three functions on its
+ * mda_qwen_t: mda_qwen_moe_mm (:770-786), mda_qwen_route_rec (:788-836) and
+ * mda_qwen_moe_rec (:838-907), with its scratch buffers and fp16 scale
+ * slots (:500-539) kept in mda_qwen_t.  These are the same three over
+ * device pointers, with that state gathered in rmda_qwen_moe_t, so that a
+ * qwen.c keeps its signatures and forwards to them.  They run the
+ * reference's sequence stage by stage (128-row segments, scaled fp16 casts,
+ * fp32 GEMM outputs); rmda_moe_layer is the fused fast path.
+ * Differences, as for the stage entry points: the router is the fp32
+ * rmda_moe_router (its p holds the experts' logits and, with a shared
+ * expert, the shared gate in column `experts`; the shared gate/up
+ * projections come from w_sh_gate_up through rmda_moe_mm instead of from
+ * further p columns).  All functions are enqueue-only, return a status and
+ * leave it sticky in ctx; nothing is allocated. */
+#define RMDA_QWEN_TILE 128u       /* MDA_QWEN_TILE, src/qwen.h:14 */
+#define RMDA_QWEN_MAX_SLOTS 16u   /* fp16 scale slots per chunk */
+
+typedef struct rmda_qwen_moe_t {
+    rmda_moe_ctx_t *ctx;
+    /* the mda_qwen_cfg_t fields the MoE uses */
+    uint32_t d;
+    uint32_t experts;
+    uint32_t topk;
+    uint32_t inter;
+    uint32_t shared;            /* 0 or the shared expert's intermediate size */
+    /* hyper-connection streams of the combine (MDA_QWEN_HC, cfg.hc_rank,
+     * MDA_QWEN_HC_PAD in the reference) */
+    uint32_t hc;
+    uint32_t hc_rank;
+    uint32_t inj_stride;
+    /* device weights */
+    const float *w_router;        /* [experts (+1 shared gate)][d] fp32 */
+    const uint16_t *w_gate_up;    /* [experts][2*inter][d] fp16 */
+    const uint16_t *w_down;       /* [experts][d][inter] fp16 */
+    const uint16_t *w_sh_gate_up; /* [2*shared][d] fp16, or NULL */
+    const uint16_t *w_sh_down;    /* [d][shared] fp16, or NULL */
+    /* device scratch of rmda_qwen_moe_scratch_bytes(q) bytes, laid out for
+     * chunks of up to max_rows rows (mda_qwen_scratch, src/qwen.c:149-185) */
+    uint32_t max_rows;
+    void *scratch;
+    size_t scratch_bytes;
+    uint32_t n_slots;             /* scale slots taken in the current chunk */
+} rmda_qwen_moe_t;
+
+/* Device views into the scratch (byte offsets), for callers and tests:
+ * p [rows][p_stride] fp32, idx/wt/slot [rows*topk], count/off [experts],
+ * xp [mrows][d] fp16, amax [RMDA_QWEN_MAX_SLOTS]. */
+typedef struct rmda_qwen_moe_layout_t {
+    size_t p;
+    size_t idx;
+    size_t wt;
+    size_t count;
+    size_t off;
+    size_t slot;
+    size_t xp;
+    size_t amax;
+    size_t total;
+    uint32_t p_stride;
+} rmda_qwen_moe_layout_t;
+
+/* Scratch bytes for q's configuration and max_rows (0 when rejected). */
+size_t rmda_qwen_moe_scratch_bytes(const rmda_qwen_moe_t *q);
+int rmda_qwen_moe_layout(const rmda_qwen_moe_t *q, rmda_qwen_moe_layout_t *out);
+
+/* mda_qwen_moe_mm: C = A . W[e]^T / (scale(sa)), 128-row tiles mapped to
+ * experts by the tile map route_rec left in the scratch. */
+int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out,
+                     uint32_t m, uint32_t n, uint32_t k);
+
+/* mda_qwen_route_rec: top-k of the scratch's p, 128-row segment offsets and
+ * tile map, and the scatter of the scaled activations into xp (whose rows
+ * are zero-filled first, src/qwen.c:793-798).  mrows = rows*topk +
+ * experts*127 rounded up to 128 (mda_qwen_moe_rows, src/qwen.c:68-70). */
+int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows);
+
+/* mda_qwen_moe_rec for one chunk of `rows` tokens of fp32 activations x
+ * [rows][d]: scale slots reset, x cast with a slot, router, route_rec,
+ * gate_up, SwiGLU, hp cast with a slot, down, the shared expert, combine.
+ * With h != NULL the combine injects into the hyper-connection streams,
+ * h[r][s][c] += y * 2 * sigmoid(inj[r*inj_stride + hc_rank + s] / hc)
+ * (shader/moe_combine.comp:36-38); with out != NULL it writes y as fp16. */
+int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, float *h, uint16_t *out,
+                      uint32_t rows);
+
 #ifdef __cplusplus
 }
 #endif

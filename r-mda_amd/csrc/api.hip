@@ -1204,3 +1204,292 @@ int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n, uint64_t
 }
 
 }  // extern "C"
+
+// ---- the qwen.c MoE recording over the stage entry points ----
+
+namespace {
+
+struct ShimPlan {
+    size_t x16, a16, p, idx, wt, count, off, fill, tiles, slot, xp, g, hp, hp16, ye;
+    size_t gs, hs, hs16, sh, tiles1, amax, total;
+    uint32_t ps, rows_pad, mrows;
+};
+
+uint32_t qwen_moe_rows(uint32_t rows, uint32_t topk, uint32_t experts) {
+    // mda_qwen_moe_rows, src/qwen.c:68-70
+    const uint64_t m = (uint64_t)rows * topk + (uint64_t)experts * (RMDA_QWEN_TILE - 1);
+    return (uint32_t)((m + RMDA_QWEN_TILE - 1) / RMDA_QWEN_TILE * RMDA_QWEN_TILE);
+}
+
+bool shim_ok(const rmda_qwen_moe_t *q) {
+    return q != nullptr && q->d > 0 && q->d % 256 == 0 && q->experts > 0 && q->experts <= RMDA_MAX_EXPERTS &&
+           q->topk > 0 && q->topk <= RMDA_MAX_TOPK && q->topk <= q->experts && q->inter > 0 &&
+           q->inter % 128 == 0 && q->shared % 128 == 0 && q->max_rows > 0 &&
+           (uint64_t)q->max_rows * q->topk <= RMDA_CTX_MAX_PAIRS && q->hc <= RMDA_MAX_HC;
+}
+
+// Scratch layout, as mda_qwen_scratch sizes its MoE buffers (src/qwen.c:166-179)
+ShimPlan plan_shim(const rmda_qwen_moe_t *q) {
+    ShimPlan p{};
+    const uint32_t T = q->max_rows, d = q->d, E = q->experts, K = q->topk, I = q->inter, S = q->shared;
+    p.ps = E + (S > 0 ? 1u : 0u);
+    p.rows_pad = (T + RMDA_QWEN_TILE - 1) / RMDA_QWEN_TILE * RMDA_QWEN_TILE;
+    p.mrows = qwen_moe_rows(T, K, E);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    p.x16 = take((size_t)T * d * 2);
+    p.a16 = take((size_t)p.rows_pad * d * 2);
+    p.p = take((size_t)T * p.ps * 4);
+    p.idx = take((size_t)T * K * 4);
+    p.wt = take((size_t)T * K * 4);
+    p.count = take((size_t)E * 4);
+    p.off = take((size_t)E * 4);
+    p.fill = take((size_t)E * 4);
+    p.tiles = take((size_t)p.mrows / RMDA_QWEN_TILE * 4);
+    p.slot = take((size_t)T * K * 4);
+    p.xp = take((size_t)p.mrows * d * 2);
+    p.g = take((size_t)p.mrows * 2 * I * 4);
+    p.hp = take((size_t)p.mrows * I * 4);
+    p.hp16 = take((size_t)p.mrows * I * 2);
+    p.ye = take((size_t)p.mrows * d * 4);
+    if (S > 0) {
+        p.gs = take((size_t)p.rows_pad * 2 * S * 4);
+        p.hs = take((size_t)p.rows_pad * S * 4);
+        p.hs16 = take((size_t)p.rows_pad * S * 2);
+        p.sh = take((size_t)p.rows_pad * d * 4);
+        p.tiles1 = take((size_t)p.rows_pad / RMDA_QWEN_TILE * 4);
+    }
+    p.amax = take((size_t)RMDA_QWEN_MAX_SLOTS * 4);
+    p.total = o;
+    return p;
+}
+
+template <typename T>
+T *scr(const rmda_qwen_moe_t *q, size_t off) {
+    return reinterpret_cast<T *>(static_cast<uint8_t *>(q->scratch) + off);
+}
+
+// entry guard of the shim: context, configuration and scratch
+int shim_enter(rmda_qwen_moe_t *q, const char *who, ShimPlan *plan) {
+    if (q == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    int rc = enter(q->ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (!shim_ok(q)) {
+        return fail(q->ctx, RMDA_ERR_SHAPE, "%s: unsupported configuration", who);
+    }
+    if (q->w_router == nullptr || q->w_gate_up == nullptr || q->w_down == nullptr ||
+        (q->shared > 0 && (q->w_sh_gate_up == nullptr || q->w_sh_down == nullptr))) {
+        return fail(q->ctx, RMDA_ERR_ARG, "%s: missing weights", who);
+    }
+    *plan = plan_shim(q);
+    if (q->scratch == nullptr || q->scratch_bytes < plan->total) {
+        return fail(q->ctx, RMDA_ERR_WORKSPACE, "%s: scratch %zu bytes < %zu", who, q->scratch_bytes, plan->total);
+    }
+    return RMDA_OK;
+}
+
+// mda_qwen_slot (src/qwen.c:505-515)
+uint32_t shim_slot(rmda_qwen_moe_t *q) {
+    if (q->n_slots >= RMDA_QWEN_MAX_SLOTS) {
+        fail(q->ctx, RMDA_ERR_SHAPE, "rmda_qwen_moe: out of fp16 scale slots");
+        return RMDA_NO_SLOT;
+    }
+    return q->n_slots++;
+}
+
+// mda_qwen_cast (src/qwen.c:517-539): absmax into a new slot, then the cast
+int shim_cast(rmda_qwen_moe_t *q, const ShimPlan &p, const float *src, uint16_t *dst, uint32_t n, uint32_t *slot) {
+    *slot = shim_slot(q);
+    if (*slot == RMDA_NO_SLOT) {
+        return q->ctx->err;
+    }
+    uint32_t *amax = scr<uint32_t>(q, p.amax);
+    const rmda_pc_absmax_t pa{n, *slot};
+    int rc = rmda_absmax(q->ctx, &pa, src, amax);
+    if (rc == RMDA_OK) {
+        const rmda_pc_cast_t pc{n, *slot};
+        rc = rmda_cast_f16(q->ctx, &pc, src, dst, amax);
+    }
+    return rc;
+}
+
+}  // namespace
+
+size_t rmda_qwen_moe_scratch_bytes(const rmda_qwen_moe_t *q) {
+    return shim_ok(q) ? plan_shim(q).total : 0;
+}
+
+int rmda_qwen_moe_layout(const rmda_qwen_moe_t *q, rmda_qwen_moe_layout_t *out) {
+    if (out == nullptr || !shim_ok(q)) {
+        return RMDA_ERR_ARG;
+    }
+    const ShimPlan p = plan_shim(q);
+    out->p = p.p;
+    out->idx = p.idx;
+    out->wt = p.wt;
+    out->count = p.count;
+    out->off = p.off;
+    out->slot = p.slot;
+    out->xp = p.xp;
+    out->amax = p.amax;
+    out->total = p.total;
+    out->p_stride = p.ps;
+    return RMDA_OK;
+}
+
+int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out, uint32_t m,
+                     uint32_t n, uint32_t k) {
+    ShimPlan p;
+    int rc = shim_enter(q, "rmda_qwen_moe_mm", &p);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (m > p.mrows) {
+        return fail(q->ctx, RMDA_ERR_SHAPE, "rmda_qwen_moe_mm: m=%u beyond the scratch's %u rows", m, p.mrows);
+    }
+    const rmda_pc_moe_mm_t pc{m, n, k, sa, RMDA_NO_SLOT};
+    return rmda_moe_mm(q->ctx, &pc, a, w, out, scr<uint32_t>(q, p.amax), scr<uint32_t>(q, p.tiles));
+}
+
+int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows) {
+    ShimPlan p;
+    int rc = shim_enter(q, "rmda_qwen_route_rec", &p);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (rows > q->max_rows || mrows != qwen_moe_rows(rows, q->topk, q->experts)) {
+        return fail(q->ctx, RMDA_ERR_SHAPE, "rmda_qwen_route_rec: rows=%u mrows=%u (max_rows %u)", rows, mrows,
+                    q->max_rows);
+    }
+    if (rows == 0) {
+        return RMDA_OK;
+    }
+    // the reference zero-fills xp (src/qwen.c:798); count, fill and the tile
+    // map need no fill here (route overwrites count, scatter takes fill as
+    // zero, scan writes every tile)
+    rc = hip_check(q->ctx, rmda_launch_zero(q->ctx->stream, scr<uint32_t>(q, p.xp), (size_t)mrows * q->d / 2, 0),
+                   "route_rec xp fill");
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    const rmda_pc_moe_route_t pr{rows, q->experts, q->topk, p.ps};
+    rc = rmda_moe_route(q->ctx, &pr, scr<float>(q, p.p), scr<uint32_t>(q, p.idx), scr<float>(q, p.wt),
+                        scr<uint32_t>(q, p.count));
+    if (rc == RMDA_OK) {
+        const rmda_pc_moe_scan_t ps{q->experts, RMDA_QWEN_TILE};
+        rc = rmda_moe_scan(q->ctx, &ps, scr<uint32_t>(q, p.count), scr<uint32_t>(q, p.off),
+                           scr<uint32_t>(q, p.tiles), mrows / RMDA_QWEN_TILE);
+    }
+    if (rc == RMDA_OK) {
+        rc = rmda_moe_scatter_experts(q->ctx, q->experts);
+    }
+    if (rc == RMDA_OK) {
+        const rmda_pc_moe_scatter_t pt{rows, q->topk, q->d / 8};
+        rc = rmda_moe_scatter(q->ctx, &pt, scr<uint32_t>(q, p.idx), scr<uint32_t>(q, p.off),
+                              scr<uint32_t>(q, p.fill), scr<uint16_t>(q, p.a16), scr<uint16_t>(q, p.xp),
+                              scr<uint32_t>(q, p.slot));
+    }
+    return rc;
+}
+
+int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, float *h, uint16_t *out,
+                      uint32_t rows) {
+    ShimPlan p;
+    int rc = shim_enter(q, "rmda_qwen_moe_rec", &p);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    rmda_moe_ctx_t *c = q->ctx;
+    if (rows > q->max_rows) {
+        return fail(c, RMDA_ERR_SHAPE, "rmda_qwen_moe_rec: rows=%u > max_rows=%u", rows, q->max_rows);
+    }
+    if (x == nullptr || (h == nullptr && out == nullptr) || (h != nullptr && (inj == nullptr || q->hc == 0))) {
+        return fail(c, RMDA_ERR_ARG, "rmda_qwen_moe_rec: x, and out or (h, inj, hc > 0), are required");
+    }
+    if (rows == 0) {
+        return RMDA_OK;
+    }
+    const uint32_t d = q->d, E = q->experts, K = q->topk, I = q->inter, S = q->shared;
+    const uint32_t mrows = qwen_moe_rows(rows, K, E);
+    const uint32_t rows_pad = (rows + RMDA_QWEN_TILE - 1) / RMDA_QWEN_TILE * RMDA_QWEN_TILE;
+    uint32_t *amax = scr<uint32_t>(q, p.amax);
+    // mda_qwen_slots_begin (src/qwen.c:500-503)
+    q->n_slots = 0;
+    rc = hip_check(c, rmda_launch_zero(c->stream, amax, RMDA_QWEN_MAX_SLOTS, 0), "moe_rec slot fill");
+    // A0: x cast with a slot for the GEMMs; the fp32 router reads x as fp16
+    uint32_t sx = RMDA_NO_SLOT;
+    if (rc == RMDA_OK) {
+        rc = shim_cast(q, p, x, scr<uint16_t>(q, p.a16), rows * d, &sx);
+    }
+    if (rc == RMDA_OK) {
+        const rmda_pc_cast_t pc{rows * d, RMDA_NO_SLOT};
+        rc = rmda_cast_f16(c, &pc, x, scr<uint16_t>(q, p.x16), amax);
+    }
+    if (rc == RMDA_OK) {
+        const rmda_moe_router_t pr{rows, d, p.ps, p.ps, 0};
+        rc = rmda_moe_router(c, &pr, scr<uint16_t>(q, p.x16), q->w_router, nullptr, scr<float>(q, p.p));
+    }
+    // A1-A3
+    if (rc == RMDA_OK) {
+        rc = rmda_qwen_route_rec(q, rows, mrows);
+    }
+    // A4-A7: gate_up, SwiGLU, hp cast with a slot, down (src/qwen.c:847-878)
+    if (rc == RMDA_OK) {
+        rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d);
+    }
+    if (rc == RMDA_OK) {
+        const rmda_pc_qwen_elem_t pe{mrows, I, 2 * I, 0, I, 0, 1.0f};
+        rc = rmda_qwen_elem(c, &pe, scr<float>(q, p.g), scr<float>(q, p.hp));
+    }
+    uint32_t sh = RMDA_NO_SLOT;
+    if (rc == RMDA_OK) {
+        rc = shim_cast(q, p, scr<float>(q, p.hp), scr<uint16_t>(q, p.hp16), mrows * I, &sh);
+    }
+    if (rc == RMDA_OK) {
+        rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.hp16), sh, q->w_down, scr<float>(q, p.ye), mrows, d, I);
+    }
+    // A8: the shared expert as one-expert grouped GEMMs over the padded rows
+    // (src/qwen.c:879-886); rows past `rows` hold stale data and are unused
+    if (rc == RMDA_OK && S > 0) {
+        uint32_t *t1 = scr<uint32_t>(q, p.tiles1);
+        rc = hip_check(c, rmda_launch_zero(c->stream, t1, rows_pad / RMDA_QWEN_TILE, 0), "moe_rec shared tiles");
+        if (rc == RMDA_OK) {
+            const rmda_pc_moe_mm_t pm{rows_pad, 2 * S, d, sx, RMDA_NO_SLOT};
+            rc = rmda_moe_mm(c, &pm, scr<uint16_t>(q, p.a16), q->w_sh_gate_up, scr<float>(q, p.gs), amax, t1);
+        }
+        if (rc == RMDA_OK) {
+            const rmda_pc_qwen_elem_t pe{rows, S, 2 * S, 0, S, 0, 1.0f};
+            rc = rmda_qwen_elem(c, &pe, scr<float>(q, p.gs), scr<float>(q, p.hs));
+        }
+        uint32_t ss = RMDA_NO_SLOT;
+        if (rc == RMDA_OK) {
+            rc = shim_cast(q, p, scr<float>(q, p.hs), scr<uint16_t>(q, p.hs16), rows * S, &ss);
+        }
+        if (rc == RMDA_OK) {
+            const rmda_pc_moe_mm_t pm{rows_pad, d, S, ss, RMDA_NO_SLOT};
+            rc = rmda_moe_mm(c, &pm, scr<uint16_t>(q, p.hs16), q->w_sh_down, scr<float>(q, p.sh), amax, t1);
+        }
+    }
+    // A9: combine (src/qwen.c:887-906)
+    if (rc == RMDA_OK) {
+        const rmda_pc_moe_combine_t pm{rows, d, K, p.ps, E, q->inj_stride, q->hc_rank, q->hc};
+        const float *shp = S > 0 ? scr<float>(q, p.sh) : nullptr;
+        if (h != nullptr) {
+            rc = rmda_moe_combine(c, &pm, scr<float>(q, p.wt), scr<uint32_t>(q, p.slot), scr<float>(q, p.ye),
+                                  scr<float>(q, p.p), shp, inj, h);
+        }
+        if (rc == RMDA_OK && out != nullptr) {
+            rc = rmda_moe_combine_plain(c, &pm, scr<float>(q, p.wt), scr<uint32_t>(q, p.slot),
+                                        scr<float>(q, p.ye), scr<float>(q, p.p), shp, out);
+        }
+    }
+    return rc;
+}

@@ -97,6 +97,20 @@ class WsLayout(ctypes.Structure):
                 ("total", ctypes.c_size_t), ("proj_stride", _u32)]
 
 
+class QwenMoe(ctypes.Structure):
+    _fields_ = [("ctx", _p), ("d", _u32), ("experts", _u32), ("topk", _u32), ("inter", _u32), ("shared", _u32),
+                ("hc", _u32), ("hc_rank", _u32), ("inj_stride", _u32), ("w_router", _p), ("w_gate_up", _p),
+                ("w_down", _p), ("w_sh_gate_up", _p), ("w_sh_down", _p), ("max_rows", _u32), ("scratch", _p),
+                ("scratch_bytes", ctypes.c_size_t), ("n_slots", _u32)]
+
+
+class QwenLayout(ctypes.Structure):
+    _fields_ = [("p", ctypes.c_size_t), ("idx", ctypes.c_size_t), ("wt", ctypes.c_size_t),
+                ("count", ctypes.c_size_t), ("off", ctypes.c_size_t), ("slot", ctypes.c_size_t),
+                ("xp", ctypes.c_size_t), ("amax", ctypes.c_size_t), ("total", ctypes.c_size_t),
+                ("p_stride", _u32)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "rmda_moe_ctx_create": (ctypes.c_int, [ctypes.POINTER(_p), ctypes.c_int, _p]),
@@ -139,6 +153,11 @@ SIGNATURES = {
     "rmda_st_find": (ctypes.c_int, [_p, ctypes.c_char_p, _p]),
     "rmda_moe_upload_layer": (ctypes.c_int, [_p, _p, ctypes.c_char_p, _p, _p]),
     "rmda_moe_upload_wait": (ctypes.c_int, [_p]),
+    "rmda_qwen_moe_scratch_bytes": (ctypes.c_size_t, [_p]),
+    "rmda_qwen_moe_layout": (ctypes.c_int, [_p, _p]),
+    "rmda_qwen_moe_mm": (ctypes.c_int, [_p, _p, _u32, _p, _p, _u32, _u32, _u32]),
+    "rmda_qwen_route_rec": (ctypes.c_int, [_p, _u32, _u32]),
+    "rmda_qwen_moe_rec": (ctypes.c_int, [_p, _p, _p, _p, _p, _u32]),
 }
 
 _LIB = None

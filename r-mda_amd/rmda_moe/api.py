@@ -257,3 +257,56 @@ def ws_views(shape, workspace):
         "off": view(lay["off"], E, torch.int32),
         "slot": view(lay["slot"], T * K, torch.int32),
     }
+
+
+class QwenMoe:
+    """rmda_qwen_moe_t: the qwen.c MoE recording (mda_qwen_moe_rec,
+    mda_qwen_route_rec, mda_qwen_moe_mm; src/qwen.c:770-907) over the stage
+    entry points, with its scratch allocated here once for max_rows."""
+
+    def __init__(self, ctx, shape, w_router, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, max_rows=None,
+                 hc=0, hc_rank=0, inj_stride=0):
+        self.ctx = ctx
+        q = _lib.QwenMoe()
+        q.ctx = ctx.h
+        q.d, q.experts, q.topk = shape["d"], shape["experts"], shape["topk"]
+        q.inter, q.shared = shape["inter"], shape["shared"]
+        q.hc, q.hc_rank, q.inj_stride = hc, hc_rank, inj_stride
+        self._keep = [w_router, w_gate_up, w_down, w_sh_gate_up, w_sh_down]
+        q.w_router, q.w_gate_up, q.w_down = _ptr(w_router), _ptr(w_gate_up), _ptr(w_down)
+        q.w_sh_gate_up, q.w_sh_down = _ptr(w_sh_gate_up), _ptr(w_sh_down)
+        q.max_rows = shape["rows"] if max_rows is None else max_rows
+        n = _lib.lib().rmda_qwen_moe_scratch_bytes(ctypes.byref(q))
+        if n == 0:
+            raise ValueError("rmda_qwen_moe_scratch_bytes rejected the configuration %r" % (shape,))
+        self.scratch = torch.empty(n, dtype=torch.uint8, device="cuda")
+        q.scratch = self.scratch.data_ptr()
+        q.scratch_bytes = n
+        self.q = q
+        lay = _lib.QwenLayout()
+        rc = _lib.lib().rmda_qwen_moe_layout(ctypes.byref(q), ctypes.byref(lay))
+        if rc != 0:
+            raise MoeError(rc, "rmda_qwen_moe_layout rejected the configuration")
+        self.layout = {k: getattr(lay, k) for k, _ in _lib.QwenLayout._fields_}
+
+    def moe_rec(self, x, rows, inj=None, h=None, out=None):
+        self.ctx._check(_lib.lib().rmda_qwen_moe_rec(ctypes.byref(self.q), _ptr(x), _ptr(inj), _ptr(h), _ptr(out),
+                                                     rows))
+
+    def views(self, rows):
+        """Typed views of the chunk's routing intermediates in the scratch."""
+        lay, q = self.layout, self.q
+        K, E = q.topk, q.experts
+
+        def view(off, n, dtype):
+            nbytes = n * torch.tensor([], dtype=dtype).element_size()
+            return self.scratch[off:off + nbytes].view(dtype)
+
+        return {
+            "p": view(lay["p"], rows * lay["p_stride"], torch.float32).view(rows, lay["p_stride"]),
+            "idx": view(lay["idx"], rows * K, torch.int32),
+            "wt": view(lay["wt"], rows * K, torch.float32),
+            "count": view(lay["count"], E, torch.int32),
+            "off": view(lay["off"], E, torch.int32),
+            "slot": view(lay["slot"], rows * K, torch.int32),
+        }

@@ -115,3 +115,36 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.lib()
+
+
+def _qwen(cfg, max_rows=None):
+    q = _lib.QwenMoe()
+    q.d, q.experts, q.topk, q.inter, q.shared = cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"], cfg["shared"]
+    q.max_rows = cfg["rows"] if max_rows is None else max_rows
+    return q
+
+
+def test_qwen_shim_scratch_sizing(L):
+    """rmda_qwen_moe_scratch_bytes / _layout: the reference's MoE scratch
+    (mda_qwen_scratch, src/qwen.c:166-179) for mrows = round(T*k + E*127, 128)."""
+    cfg = configs.CONFIGS[3]
+    q = _qwen(cfg)
+    n = L.rmda_qwen_moe_scratch_bytes(ctypes.byref(q))
+    T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
+    mrows = (T * K + E * 127 + 127) // 128 * 128
+    assert mrows == 32640  # SURVEY's config-3 figure (255 tiles)
+    # xp, g, hp, hp16 and ye alone
+    assert n >= mrows * d * 2 + mrows * 2 * I * 4 + mrows * I * 6 + mrows * d * 4
+    lay = _lib.QwenLayout()
+    assert L.rmda_qwen_moe_layout(ctypes.byref(q), ctypes.byref(lay)) == 0
+    assert lay.total == n and lay.p_stride == E
+    offs = [lay.p, lay.idx, lay.wt, lay.count, lay.off, lay.slot, lay.xp, lay.amax]
+    assert all(o % 256 == 0 for o in offs) and len(set(offs)) == len(offs) and max(offs) < n
+    # a shared expert adds the gate column to p
+    q5 = _qwen(configs.CONFIGS[5], max_rows=512)
+    assert L.rmda_qwen_moe_layout(ctypes.byref(q5), ctypes.byref(lay)) == 0 and lay.p_stride == 513
+    # rejected configurations size to 0
+    for field, bad in [("d", 100), ("topk", 0), ("inter", 96), ("experts", 600), ("max_rows", 0), ("shared", 64)]:
+        qb = _qwen(cfg)
+        setattr(qb, field, bad)
+        assert L.rmda_qwen_moe_scratch_bytes(ctypes.byref(qb)) == 0, field

@@ -1,0 +1,129 @@
+"""The qwen.c MoE recording (rmda_qwen_moe_rec, rmda_qwen_route_rec,
+rmda_qwen_moe_mm; src/qwen.c:770-907) against the CPU oracle's layer in the
+reference's own mode: 128-row segments (mda_qwen_moe_rows), activations and
+SwiGLU outputs cast to fp16 with power-of-two slot scales (src/qwen.c:500-539,
+absmax.comp + cast_f16.comp) that the next GEMM divides out.
+
+Routing intermediates are bit-exact (logits, expert indices, counts, 128-row
+offsets, slots); the output is within the layer's tolerance.  The scratch is
+filled with NaN bytes first, so a stage that leaves its part of the chain
+unwritten shows up."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import MAX_ABS, REL_L2, out_metrics, u32
+from oracle import oracle as orc
+from rmda_moe import api, configs, inputs
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    configs.CONFIGS[1],  # tiny: 8 experts, top-2
+    configs.CONFIGS[2],  # decode: 128 experts, top-8, T = 128
+    dict(name="shared_small", rows=200, d=256, experts=16, topk=4, inter=128, shared=128, skew=False),
+    dict(name="ragged_k5", rows=77, d=512, experts=24, topk=5, inter=256, shared=0, skew=False),
+]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    torch.cuda.set_device(0)
+    c = api.Context(0)
+    yield c
+    c.close()
+
+
+def make_shim(ctx, inp, **kw):
+    return api.QwenMoe(ctx, inp["shape"], inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                       inp["w_sh_down"], **kw)
+
+
+@pytest.mark.parametrize("cfg", SHAPES, ids=[c["name"] for c in SHAPES])
+def test_moe_rec_matches_oracle_reference_mode(ctx, cfg):
+    print("shim %s" % cfg["name"], flush=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=3)
+    T, d = cfg["rows"], cfg["d"]
+    q = make_shim(ctx, inp)
+    q.scratch.fill_(255)
+    out = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
+    q.moe_rec(inp["x"].float(), T, out=out)
+    ctx.sync()
+    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1)
+    v = q.views(T)
+    assert np.array_equal(v["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(v["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(v["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(v["off"]), ref["off"]), "128-row segment offsets"
+    assert np.array_equal(u32(v["slot"]), ref["slot"]), "permutation"
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    max_abs, rel = out_metrics(got, ref["out"])
+    print("  max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+    # three fp16 scale slots were taken: x, hp and (with a shared expert) hs
+    assert q.q.n_slots == (3 if cfg["shared"] else 2)
+
+
+def test_moe_rec_hyper_connection_streams(ctx):
+    """h[r, s, c] += y[r, c] * 2 * sigmoid(inj[r, hc_rank + s] / hc), the
+    reference's combine epilogue (shader/moe_combine.comp:36-38), against the
+    oracle's y; the plain output of the same call is the y the streams got."""
+    cfg = dict(name="hc", rows=96, d=256, experts=12, topk=3, inter=128, shared=128, skew=False)
+    inp = inputs.make_inputs(ctx, cfg, seed=5)
+    T, d, hc, stride, rank = cfg["rows"], cfg["d"], 4, 10, 3
+    q = make_shim(ctx, inp, hc=hc, hc_rank=rank, inj_stride=stride)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    h0 = torch.randn(T, hc, d, device="cuda", generator=g)
+    inj = torch.randn(T, stride, device="cuda", generator=g) * 3
+    h = h0.clone()
+    out = torch.empty(T, d, dtype=torch.float16, device="cuda")
+    q.moe_rec(inp["x"].float(), T, inj=inj, h=h, out=out)
+    ctx.sync()
+    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1)
+    gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[:, rank:rank + hc] / hc))
+    want = h0.cpu().numpy().astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]
+    err = np.abs(h.cpu().numpy().astype(np.float64) - want).max()
+    print("  hc max-abs %.3g" % err, flush=True)
+    assert err <= 2 * MAX_ABS, err
+    max_abs, rel = out_metrics(out.float().cpu().numpy(), ref["out"])
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_moe_rec_runs_twice_bitwise_and_chunks(ctx):
+    """Run-to-run determinism, and a smaller second chunk through the same
+    scratch (laid out for max_rows) gives the oracle's answer for that chunk."""
+    cfg = configs.CONFIGS[1]
+    inp = inputs.make_inputs(ctx, cfg, seed=7)
+    T, d = cfg["rows"], cfg["d"]
+    q = make_shim(ctx, inp)
+    outs = []
+    for _ in range(2):
+        out = torch.empty(T, d, dtype=torch.float16, device="cuda")
+        q.moe_rec(inp["x"].float(), T, out=out)
+        ctx.sync()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    n = 100
+    small = dict(cfg, rows=n)
+    sub = {k: (v[:n] if k == "x" else v) for k, v in inp.items()}
+    sub["shape"] = configs.shape_of(small)
+    out = torch.empty(n, d, dtype=torch.float16, device="cuda")
+    q.moe_rec(inp["x"][:n].float().contiguous(), n, out=out)
+    ctx.sync()
+    ref = orc.layer(inputs.to_host(sub), tile=128, hp_scale=1, x_scale=1)
+    max_abs, rel = out_metrics(out.float().cpu().numpy(), ref["out"])
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_moe_rec_rejects_bad_calls(ctx):
+    cfg = configs.CONFIGS[1]
+    inp = inputs.make_inputs(ctx, cfg, seed=1)
+    q = make_shim(ctx, inp, max_rows=64)
+    out = torch.empty(cfg["rows"], cfg["d"], dtype=torch.float16, device="cuda")
+    with pytest.raises(api.MoeError):
+        q.moe_rec(inp["x"].float(), cfg["rows"], out=out)  # more rows than the scratch holds
+    ctx.clear_error()
+    with pytest.raises(api.MoeError):
+        q.moe_rec(inp["x"].float(), 64)  # neither out nor h
+    ctx.clear_error()
