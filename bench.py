@@ -295,6 +295,24 @@ def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
         res[name] = {"us": round(us, 2), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), "bytes": nbytes,
                      "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     del g32, hp16, ye32
+    # the whole reference-structured recording (mda_qwen_moe_rec's sequence
+    # over these entry points), fp32 activations in, hc streams out
+    from rmda_moe import api
+    qm = api.QwenMoe(ctx, s, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                     inp["w_sh_down"], hc=HC, hc_rank=0, inj_stride=HC_PAD)
+    x32 = inp["x"].float()
+    for _ in range(3):
+        qm.moe_rec(x32, T, inj=inj, h=h)
+    ctx.sync()
+    e0.record()
+    for _ in range(10):
+        qm.moe_rec(x32, T, inj=inj, h=h)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    res["qwen_moe_rec"] = {"ms_per_step": round(ms, 4), "tokens/s": round(T / (ms * 1e-3), 1),
+                           "what": "rmda_qwen_moe_rec: the reference's recording stage by stage, HF weights"}
+    del qm, x32
     sc_b = res["scatter"]["bytes"] + res["combine_hc"]["bytes"]
     sc_us = res["scatter"]["us"] + res["combine_hc"]["us"]
     res["scatter+combine_hc_GB/s"] = round(sc_b / (sc_us * 1e-6) / 1e9, 1)
