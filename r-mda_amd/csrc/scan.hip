@@ -161,18 +161,21 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     // completed (vmcnt(0)) before the block takes its ticket, so the last
     // block sees every total without a device-scope fence: on this multi-XCD
     // part such a fence writes back and invalidates the whole L2.
-    for (uint32_t e = tid; e < E; e += NT) {
-        __hip_atomic_store(&a.hist[(size_t)b * E + e], run[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        // atomicInc wraps the ticket back to 0 on the last block
-        s_last = atomicInc(a.done, nb - 1) == nb - 1;
-    }
-    __syncthreads();
-    if (!s_last) {
-        return;
+    // A single block needs no hand-off: its own counts (run[]) are the totals.
+    if (nb > 1) {
+        for (uint32_t e = tid; e < E; e += NT) {
+            __hip_atomic_store(&a.hist[(size_t)b * E + e], run[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            // atomicInc wraps the ticket back to 0 on the last block
+            s_last = atomicInc(a.done, nb - 1) == nb - 1;
+        }
+        __syncthreads();
+        if (!s_last) {
+            return;
+        }
     }
 
     // Each thread owns experts e0 = 2t and e0+1.  Pass 1: column totals of
@@ -196,12 +199,24 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     };
     uint32_t c0 = 0;
     uint32_t c1 = 0;
-    for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
-        load_batch(bb0);
+    if (nb == 1) {
 #pragma unroll
         for (uint32_t u = 0; u < RB; u += 1) {
-            c0 += h0[u];
-            c1 += h1[u];
+            h0[u] = 0u;
+            h1[u] = 0u;
+        }
+        h0[0] = own0 ? run[e0] : 0u;
+        h1[0] = own1 ? run[e0 + 1] : 0u;
+        c0 = h0[0];
+        c1 = h1[0];
+    } else {
+        for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+            load_batch(bb0);
+#pragma unroll
+            for (uint32_t u = 0; u < RB; u += 1) {
+                c0 += h0[u];
+                c1 += h1[u];
+            }
         }
     }
     const uint32_t p0 = (c0 + a.tile - 1u) / a.tile * a.tile;
