@@ -493,6 +493,11 @@ int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc, const
     if (pc->topk == 0 || pc->topk > RMDA_MAX_TOPK || (xp != nullptr && pc->d8 == 0)) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_scatter: topk=%u d8=%u", pc->topk, pc->d8);
     }
+    if (xp != nullptr && npairs <= RMDA_SCATTER1_MAX_PAIRS) {
+        return hip_check(ctx, rmda_launch_scatter1(ctx->stream, idx, off, fill, pc->rows, pc->topk,
+                                                   ctx->scatter_experts, slot, x16, xp, pc->d8),
+                         "scatter");
+    }
     rmda_rank_args_t ra{};
     ra.idx = idx;
     ra.npairs = (uint32_t)npairs;

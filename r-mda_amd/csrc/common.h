@@ -219,6 +219,12 @@ hipError_t rmda_launch_permute(hipStream_t s, const uint32_t *idx, const uint32_
                                const uint32_t *boff, uint32_t npairs, uint32_t topk,
                                uint32_t experts, uint32_t *slot, uint32_t *rowtok,
                                const uint16_t *x16, uint16_t *xp, uint32_t d8);
+// scatter.hip: the drop-in scatter with row copy in one launch (each block
+// counts the pairs before its own); O(npairs^2) L2 reads in all, so bounded.
+#define RMDA_SCATTER1_MAX_PAIRS (1u << 16)
+hipError_t rmda_launch_scatter1(hipStream_t s, const uint32_t *idx, const uint32_t *off, uint32_t *fill,
+                                uint32_t rows, uint32_t topk, uint32_t experts, uint32_t *slot,
+                                const uint16_t *x16, uint16_t *xp, uint32_t d8);
 
 // gemm.hip: grouped GEMM over a device work list.
 enum {

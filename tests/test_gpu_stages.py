@@ -200,10 +200,14 @@ def test_scan_bitexact(ctx, experts, tile):
 @pytest.mark.parametrize("rows,experts,topk,d,mode", [
     (2048, 128, 8, 2048, "route"),   # config-3 sized
     (256, 8, 2, 512, "route"),       # config 1
-    (1000, 64, 4, 256, "random"),    # arbitrary idx with repeats and NONE
+    (1001, 64, 4, 256, "random"),    # arbitrary idx with repeats and NONE; a ragged last block of tokens
     (4096, 512, 10, 128, "route"),   # several rank blocks, 512 experts
+    (777, 32, 3, 128, "unaligned"),  # idx not 16-byte aligned: the one-launch path's scalar-load variant
+    (9000, 128, 8, 64, "route"),     # 72 000 pairs: above the one-launch bound, rank then permute
 ])
 def test_scatter_bitexact(ctx, rows, experts, topk, d, mode):
+    """Both scatter paths (one launch up to RMDA_SCATTER1_MAX_PAIRS pairs,
+    rank + permute above) against the oracle's sequential scatter."""
     r = rng(rows + d)
     if mode == "route":
         p = r.standard_normal((rows, experts)).astype(np.float32)
@@ -221,7 +225,13 @@ def test_scatter_bitexact(ctx, rows, experts, topk, d, mode):
     fill = empty_u32(experts, fill=777)
     slot = empty_u32(rows * topk)
     xp = torch.zeros(mrows, d, dtype=torch.float16, device="cuda")
-    ctx.scatter(rows, topk, d // 8, dev(idx_r), dev(off_r), fill, dev(x), xp, slot)
+    idx_d = dev(idx_r)
+    if mode == "unaligned":
+        buf = torch.empty(idx_r.size + 1, dtype=idx_d.dtype, device="cuda")
+        buf[1:] = idx_d
+        idx_d = buf[1:]
+        assert idx_d.data_ptr() % 16 != 0
+    ctx.scatter(rows, topk, d // 8, idx_d, dev(off_r), fill, dev(x), xp, slot)
     ctx.sync()
     assert np.array_equal(u32(slot), slot_r)
     assert np.array_equal(u32(fill), fill_r)
