@@ -107,6 +107,20 @@ def test_layer_more_shapes(ctx, cfg):
     check_layer(ctx, cfg, seed=3)
 
 
+@pytest.mark.parametrize("cfg", [
+    # 524 288 pairs: 512 rank blocks hand their counts to the last one, and
+    # about 2 800 work items of up to 192 rows are dealt over the persistent grid
+    dict(name="large_uniform", rows=65536, d=256, experts=128, topk=8, inter=128, shared=0, skew=False),
+    # skewed: 61 of 64 experts empty, one expert with all 32 768 tokens (171
+    # items), plus a 32 768-row shared-expert group
+    dict(name="large_skew_shared", rows=32768, d=512, experts=64, topk=2, inter=256, shared=256, skew=True),
+])
+def test_layer_large(ctx, cfg):
+    """Sizes far above the benchmark configurations: routing bit-exact on
+    every token, output within tolerance on a sample of rows."""
+    check_layer(ctx, cfg, seed=7, n_sample=32)
+
+
 def test_layer_other_seed_and_ragged(ctx):
     cfg = dict(configs.CONFIGS[1], rows=203, name="ragged")
     check_layer(ctx, cfg, seed=5)
