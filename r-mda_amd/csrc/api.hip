@@ -770,6 +770,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         rc = prof_mark(ctx, RMDA_STAGE_ROUTE + 1);
     }
     // A2 counts, offsets, block bases and the GEMM work list
+    bool self_perm = false;
     if (rc == RMDA_OK) {
         rmda_rank_args_t ra{};
         ra.idx = idx;
@@ -786,11 +787,15 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.bm = RMDA_GEMM2_BM;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.sh_row0;
-        if (p.nblocks == 1) {
-            // all pairs in one rank block: it writes the permutation too
+        // all pairs in one rank block, or few enough pairs that every block
+        // counts them all: the rank blocks write the permutation too
+        self_perm = p.nblocks == 1 ||
+                    (p.npairs <= RMDA_RANK_ALL_MAX && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0);
+        if (self_perm) {
             ra.slot = slot;
             ra.rowtok = rowtok;
             ra.topk = K;
+            ra.count_all = p.nblocks > 1 ? 1u : 0u;
         }
         rc = hip_check(ctx, rmda_launch_rank(s, &ra), "layer rank");
     }
@@ -798,7 +803,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         rc = prof_mark(ctx, RMDA_STAGE_RANK + 1);
     }
     // A3 permutation (slots + row -> token map; x is gathered, not copied)
-    if (rc == RMDA_OK && p.nblocks > 1) {
+    if (rc == RMDA_OK && !self_perm) {
         rc = hip_check(ctx,
                        rmda_launch_permute(s, idx, lrank, at<uint32_t>(ws, p.hist), p.npairs, K, E, slot, rowtok,
                                            nullptr, nullptr, 0),

@@ -210,7 +210,14 @@ struct rmda_rank_args_t {
     uint32_t *slot;     // [npairs], or NULL
     uint32_t *rowtok;   // [sorted rows] row -> token, or NULL
     uint32_t topk;
+    // nonzero: every block counts all npairs itself (LDS histograms of the
+    // pairs before and after it), so no block waits for another, the blocks
+    // write slot/rowtok themselves (slot must be set), block 0 writes
+    // count/off/the work list, and hist/done are not used.  O(npairs) L2
+    // reads per block: for npairs <= RMDA_RANK_ALL_MAX; idx 16-byte aligned.
+    uint32_t count_all;
 };
+#define RMDA_RANK_ALL_MAX (1u << 16)
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);
 
 // scatter.hip: slot[pr] = boff[pr/BLOCK][e] + lrank[pr]; optional row copy

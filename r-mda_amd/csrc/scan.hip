@@ -10,6 +10,11 @@
 // finish (atomic ticket) converts hist into per-block base offsets, writes
 // off/count, and builds the grouped-GEMM work list, so the whole ranking is
 // one launch with no host round trip and no atomic-order dependence.
+// Two shortcuts skip the hand-off: a single block's counts are the totals,
+// and with count_all (up to RMDA_RANK_ALL_MAX pairs) every block also counts
+// the pairs before and after its own in LDS, which gives it the totals and
+// its own bases.  In both cases the blocks write slot and rowtok themselves
+// (no permutation launch), and block 0 alone writes the shared outputs.
 #include "common.h"
 
 namespace {
@@ -104,15 +109,57 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     __shared__ uint32_t cls_n[RMDA_ITEM_CLASSES];  // work-list items per 16-row class
     __shared__ uint32_t cls_b[RMDA_ITEM_CLASSES];
     __shared__ uint32_t sh_slot[2];
+    __shared__ uint32_t pre[RMDA_MAX_EXPERTS];   // count_all: pairs before this block
+    __shared__ uint32_t post[RMDA_MAX_EXPERTS];  // count_all: pairs after it
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = tid / RMDA_WAVE;
     const uint32_t E = a.experts;
     const uint32_t b = blockIdx.x;
     const uint32_t nb = gridDim.x;
+    // every block counts every pair itself: no hand-off, and each block
+    // writes its own slots (see rmda_rank_args_t::count_all)
+    const bool all = a.count_all != 0 && nb > 1;
+    // this kernel writes the slots itself (below), so lrank is not needed
+    const bool self_slots = a.slot != nullptr && (nb == 1 || all);
 
     for (uint32_t e = tid; e < E; e += NT) {
         run[e] = 0;
+        pre[e] = 0;
+        post[e] = 0;
+    }
+    // count_all: the other blocks' pairs as 16-byte words, CB per thread per
+    // batch; the first batch is issued now and lands during the ranking
+    // below (idx was written on other XCDs, so these loads miss L2)
+    constexpr uint32_t CB = 16;
+    const uint4 *iv = reinterpret_cast<const uint4 *>(a.idx);
+    const uint32_t n4 = a.npairs / 4;
+    const uint32_t own_lo = b * (RMDA_RANK_BLOCK / 4);
+    const uint32_t own_hi = own_lo + RMDA_RANK_BLOCK / 4;
+    uint4 cv[CB];
+    auto count_load = [&](uint32_t i0) {
+#pragma unroll
+        for (uint32_t u = 0; u < CB; u += 1) {
+            const uint32_t j = i0 + u * NT;
+            cv[u] = (j < n4 && (j < own_lo || j >= own_hi)) ? iv[j]
+                                                           : make_uint4(RMDA_NONE, RMDA_NONE, RMDA_NONE, RMDA_NONE);
+        }
+    };
+    auto count_add = [&](uint32_t i0) {
+#pragma unroll
+        for (uint32_t u = 0; u < CB; u += 1) {
+            uint32_t *h = i0 + u * NT < own_lo ? pre : post;
+            const uint32_t q[4] = {cv[u].x, cv[u].y, cv[u].z, cv[u].w};
+#pragma unroll
+            for (uint32_t t = 0; t < 4; t += 1) {
+                if (q[t] < E) {
+                    atomicAdd(&h[q[t]], 1u);
+                }
+            }
+        }
+    };
+    if (all) {
+        count_load(tid);
     }
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (RMDA_WAVE - lane));
     // all of the thread's experts are loaded up front: one memory round trip
@@ -143,7 +190,9 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
                 r += __popcll(msk[ww][e]);
             }
             r += __popcll(msk[w][e] & below);
-            a.lrank[pr] = r;
+            if (!self_slots) {
+                a.lrank[pr] = r;  // for the permutation kernel
+            }
             lr[it] = r;
         }
         __syncthreads();
@@ -162,7 +211,22 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     // block sees every total without a device-scope fence: on this multi-XCD
     // part such a fence writes back and invalidates the whole L2.
     // A single block needs no hand-off: its own counts (run[]) are the totals.
-    if (nb > 1) {
+    if (all) {
+        count_add(tid);
+        for (uint32_t i0 = tid + CB * NT; i0 < n4; i0 += CB * NT) {
+            count_load(i0);
+            count_add(i0);
+        }
+        // the last npairs % 4 pairs (past the 16-byte words) are the last
+        // block's own, i.e. after every other block
+        if (b + 1 < nb && tid < a.npairs - 4 * n4) {
+            const uint32_t e = a.idx[4 * n4 + tid];
+            if (e < E) {
+                atomicAdd(&post[e], 1u);
+            }
+        }
+        __syncthreads();
+    } else if (nb > 1) {
         for (uint32_t e = tid; e < E; e += NT) {
             __hip_atomic_store(&a.hist[(size_t)b * E + e], run[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -199,14 +263,14 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     };
     uint32_t c0 = 0;
     uint32_t c1 = 0;
-    if (nb == 1) {
+    if (nb == 1 || all) {
 #pragma unroll
         for (uint32_t u = 0; u < RB; u += 1) {
             h0[u] = 0u;
             h1[u] = 0u;
         }
-        h0[0] = own0 ? run[e0] : 0u;
-        h1[0] = own1 ? run[e0 + 1] : 0u;
+        h0[0] = own0 ? pre[e0] + run[e0] + post[e0] : 0u;
+        h1[0] = own1 ? pre[e0 + 1] + run[e0 + 1] + post[e0 + 1] : 0u;
         c0 = h0[0];
         c1 = h1[0];
     } else {
@@ -229,7 +293,8 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         o0 = own0 ? a.off_in[e0] : 0u;
         o1 = own1 ? a.off_in[e0 + 1] : 0u;
     }
-    if (own0) {
+    const bool lead = !all || b == 0;  // the block that writes the shared outputs
+    if (own0 && lead) {
         if (a.off != nullptr) {
             a.off[e0] = o0;
         }
@@ -237,7 +302,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             a.count[e0] = c0;
         }
     }
-    if (own1) {
+    if (own1 && lead) {
         if (a.off != nullptr) {
             a.off[e0 + 1] = o1;
         }
@@ -245,22 +310,22 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             a.count[e0 + 1] = c1;
         }
     }
-    if (a.slot != nullptr && nb == 1) {
-        // One block holds every pair: it writes the permutation itself,
-        // slot = off[e] + local rank, and the row -> token map, so the
-        // separate permutation launch is not needed.  run[] (this block's
-        // counts, already stored) now holds the offsets.
+    if (self_slots) {
+        // The block knows its pairs' bases: it writes the permutation itself,
+        // slot = off[e] + pairs of e before the block + local rank, and the
+        // row -> token map, so the separate permutation launch is not needed.
+        // run[] (this block's counts, no longer needed) now holds the bases.
         __syncthreads();
         if (own0) {
-            run[e0] = o0;
+            run[e0] = o0 + pre[e0];
         }
         if (own1) {
-            run[e0 + 1] = o1;
+            run[e0 + 1] = o1 + pre[e0 + 1];
         }
         __syncthreads();
 #pragma unroll
         for (uint32_t it = 0; it < ITS; it += 1) {
-            const uint32_t pr = it * NT + tid;
+            const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
             if (pr < a.npairs) {
                 const uint32_t e = ev[it];
                 const uint32_t sl = e < E ? run[e] + lr[it] : RMDA_NONE;
@@ -271,9 +336,12 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             }
         }
     }
+    if (all && b != 0) {
+        return;  // block 0 writes the work list
+    }
     uint32_t acc0 = o0;
     uint32_t acc1 = o1;
-    for (uint32_t bb0 = 0; bb0 < nb; bb0 += RB) {
+    for (uint32_t bb0 = 0; bb0 < nb && !all; bb0 += RB) {
         if (nb > RB) {
             load_batch(bb0);
         }
