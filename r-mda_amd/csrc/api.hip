@@ -418,7 +418,11 @@ int rmda_moe_route(rmda_moe_ctx_t *ctx, const rmda_pc_moe_route_t *pc, const flo
         rc = hip_check(ctx, rmda_launch_route(ctx->stream, proj, idx, wt, nullptr, pc->rows, pc->experts, pc->topk,
                                               pc->stride),
                        "route");
-        if (rc == RMDA_OK) {
+        if (rc == RMDA_OK && npairs <= RMDA_COUNT1_MAX_PAIRS) {
+            // one workgroup's LDS histogram: no hand-off between blocks
+            rc = hip_check(ctx, rmda_launch_count(ctx->stream, idx, (uint32_t)npairs, pc->experts, count),
+                           "route counts");
+        } else if (rc == RMDA_OK) {
             rmda_rank_args_t ra{};
             ra.idx = idx;
             ra.npairs = (uint32_t)npairs;

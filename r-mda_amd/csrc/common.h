@@ -219,6 +219,11 @@ struct rmda_rank_args_t {
 };
 #define RMDA_RANK_ALL_MAX (1u << 16)
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);
+// scan.hip: count[e] = |{pr < npairs : idx[pr] == e}| in one workgroup (an
+// LDS histogram); for up to RMDA_COUNT1_MAX_PAIRS pairs
+#define RMDA_COUNT1_MAX_PAIRS (1u << 16)
+hipError_t rmda_launch_count(hipStream_t s, const uint32_t *idx, uint32_t npairs, uint32_t experts,
+                             uint32_t *count);
 
 // scatter.hip: slot[pr] = boff[pr/BLOCK][e] + lrank[pr]; optional row copy
 // (xp) and inverse map (rowtok[slot] = token).

@@ -421,7 +421,66 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     }
 }
 
+// count[e] = number of idx[0, npairs) equal to e, for up to
+// RMDA_COUNT1_MAX_PAIRS pairs: one 1024-thread block, an LDS histogram, no
+// hand-off between blocks.  Four 16-byte loads per thread in flight when idx
+// is 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(1024) void count_kernel(const uint32_t *__restrict__ idx, uint32_t npairs,
+                                                     uint32_t experts, uint32_t *__restrict__ count) {
+    __shared__ uint32_t h[RMDA_MAX_EXPERTS];
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t e = tid; e < experts; e += 1024) {
+        h[e] = 0;
+    }
+    __syncthreads();
+    uint32_t done = 0;
+    if (VEC) {
+        const uint4 *iv = reinterpret_cast<const uint4 *>(idx);
+        const uint32_t n4 = npairs / 4;
+        for (uint32_t i = tid; i < n4; i += 4 * 1024) {
+            uint4 v[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u += 1) {
+                const uint32_t j = i + u * 1024;
+                v[u] = j < n4 ? iv[j] : make_uint4(RMDA_NONE, RMDA_NONE, RMDA_NONE, RMDA_NONE);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u += 1) {
+                const uint32_t q[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (uint32_t t = 0; t < 4; t += 1) {
+                    if (q[t] < experts) {
+                        atomicAdd(&h[q[t]], 1u);
+                    }
+                }
+            }
+        }
+        done = 4 * n4;
+    }
+    for (uint32_t i = done + tid; i < npairs; i += 1024) {
+        const uint32_t e = idx[i];
+        if (e < experts) {
+            atomicAdd(&h[e], 1u);
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < experts; e += 1024) {
+        count[e] = h[e];
+    }
+}
+
 }  // namespace
+
+hipError_t rmda_launch_count(hipStream_t s, const uint32_t *idx, uint32_t npairs, uint32_t experts,
+                             uint32_t *count) {
+    if ((reinterpret_cast<uintptr_t>(idx) & 15u) == 0) {
+        hipLaunchKernelGGL(count_kernel<true>, dim3(1), dim3(1024), 0, s, idx, npairs, experts, count);
+    } else {
+        hipLaunchKernelGGL(count_kernel<false>, dim3(1), dim3(1024), 0, s, idx, npairs, experts, count);
+    }
+    return hipGetLastError();
+}
 
 hipError_t rmda_launch_zero(hipStream_t s, uint32_t *p, size_t n, uint32_t value) {
     if (n == 0) {

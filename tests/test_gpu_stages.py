@@ -157,6 +157,25 @@ def test_route_bitexact(ctx, rows, experts, topk, stride):
     np.testing.assert_allclose(wt.cpu().numpy(), wt_r, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("rows,experts,topk,shift", [
+    (9000, 128, 8, 0),   # 72 000 pairs: above the one-workgroup count, counted by the rank kernel
+    (5001, 64, 4, 1),    # idx one word past 16-byte alignment: the count kernel's scalar-load variant
+])
+def test_route_counts_both_paths(ctx, rows, experts, topk, shift):
+    p = planted_logits(rows, experts, experts, seed=rows)
+    idx_r, wt_r, cnt_r = orc.route(p, experts, topk)
+    buf = empty_u32(rows * topk + shift)
+    idx = buf[shift:]
+    assert (idx.data_ptr() % 16 == 0) == (shift == 0)
+    wt = torch.empty(rows * topk, dtype=torch.float32, device="cuda")
+    cnt = empty_u32(experts, fill=777)
+    ctx.route(rows, experts, topk, experts, dev(p), idx, wt, cnt)
+    ctx.sync()
+    assert np.array_equal(u32(idx), idx_r)
+    assert np.array_equal(u32(cnt), cnt_r)
+    assert int(u32(cnt).sum()) == rows * topk
+
+
 def test_route_unselectable_rows(ctx):
     # fewer selectable columns than topk: the remaining picks are RMDA_NONE
     rows, experts, topk = 4, 8, 4
