@@ -184,7 +184,8 @@ int rmda_moe_scan(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scan_t *pc,
  * targets are not written (the reference zero-fills them first,
  * src/qwen.c:798; rmda_moe_mm never reads them as valid data).
  * `experts` is taken from the context's last rmda_moe_route call unless set
- * with rmda_moe_scatter_experts().  Requires rows*topk <= RMDA_CTX_MAX_PAIRS. */
+ * with rmda_moe_scatter_experts().  Requires rows*topk <= RMDA_CTX_MAX_PAIRS
+ * and 16-byte aligned x16 and xp. */
 int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc,
                      const uint32_t *idx, const uint32_t *off, uint32_t *fill,
                      const uint16_t *x16, uint16_t *xp, uint32_t *slot);
@@ -197,7 +198,7 @@ int rmda_moe_scatter_experts(rmda_moe_ctx_t *ctx, uint32_t experts);
  * B is [experts][n][k] fp16 (HF [out, in] per expert).  Rows of tiles marked
  * RMDA_NONE are not written.  amax holds the fp16 scale slots (may be NULL if
  * sa == sb == RMDA_NO_SLOT).  Requires m % 128 == 0, n % 128 == 0,
- * k % 32 == 0 (the reference's grid and K-step). */
+ * k % 32 == 0 (the reference's grid and K-step) and 16-byte aligned a, b, c. */
 int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc,
                 const uint16_t *a, const uint16_t *b, float *c,
                 const uint32_t *amax, const uint32_t *tiles);
@@ -271,6 +272,9 @@ typedef struct rmda_moe_shape_t {
     uint32_t shared;  /* shared expert intermediate size I_s, 0 = none */
 } rmda_moe_shape_t;
 
+/* Alignment: x, the weights, packed, out, h and workspace must be 16-byte
+ * aligned, bias and inj 4-byte aligned (RMDA_ERR_ARG otherwise), like the
+ * reference's storage-buffer offsets. */
 typedef struct rmda_moe_layer_args_t {
     const uint16_t *x;          /* rows x d fp16 activations */
     const float *w_router;      /* (experts [+1 shared gate]) x d fp32 */

@@ -85,6 +85,10 @@ int hip_check(rmda_moe_ctx_t *c, hipError_t e, const char *what) {
     return RMDA_OK;
 }
 
+// true when p (NULL allowed) is a multiple of a bytes: the kernels' 16-byte
+// vector loads and LDS DMA need 16-byte aligned rows
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
 size_t align256(size_t x) {
     return (x + 255) & ~(size_t)255;
 }
@@ -486,6 +490,9 @@ int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc, const
         (xp != nullptr && x16 == nullptr)) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scatter: null argument");
     }
+    if (!aligned(x16, 16) || !aligned(xp, 16)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scatter: x16 and xp must be 16-byte aligned");
+    }
     if (ctx->scatter_experts == 0) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_scatter: expert count unknown (call rmda_moe_route or "
                                        "rmda_moe_scatter_experts first)");
@@ -532,6 +539,9 @@ int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t 
     if (pc == nullptr || a == nullptr || b == nullptr || c == nullptr || tiles == nullptr ||
         (amax == nullptr && (pc->sa != RMDA_NO_SLOT || pc->sb != RMDA_NO_SLOT))) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_mm: null argument");
+    }
+    if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_mm: a, b and c must be 16-byte aligned");
     }
     if (pc->m % RMDA_MM_TILE != 0 || pc->n == 0 || pc->n % RMDA_MM_TILE != 0 || pc->k == 0 || pc->k % 32 != 0) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_mm: m=%u n=%u k=%u (need m,n %% 128 == 0, k %% 32 == 0)", pc->m,
@@ -705,6 +715,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: hyper-connection streams need inj and 1 <= hc <= %u "
                     "with inj_off + hc <= inj_stride (hc=%u, inj_off=%u, inj_stride=%u)", RMDA_MAX_HC, args->hc,
                     args->inj_off, args->inj_stride);
+    }
+    if (!aligned(args->x, 16) || !aligned(args->w_router, 16) || !aligned(args->w_gate_up, 16) ||
+        !aligned(args->w_down, 16) || !aligned(args->w_sh_gate_up, 16) || !aligned(args->w_sh_down, 16) ||
+        !aligned(args->packed, 16) || !aligned(args->out, 16) || !aligned(args->workspace, 16) ||
+        !aligned(args->h, 16) || !aligned(args->bias, 4) || !aligned(args->inj, 4)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: x, weights, out, h and workspace must be 16-byte aligned");
     }
     char why[128];
     if (!check_shape(shape, why, sizeof(why))) {

@@ -227,7 +227,11 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
     if (n == 0) {
         return hipSuccess;
     }
-    if (pc->d % 4 == 0 && pc->topk <= RMDA_MAX_TOPK && pc->hc <= RMDA_MAX_HC) {
+    // the vector kernel reads y, sh and h as float4 and writes out as 8-byte
+    // words; other alignments take the per-element kernel
+    const auto al = [](const void *q, uintptr_t a) { return (reinterpret_cast<uintptr_t>(q) & (a - 1)) == 0; };
+    const bool vec_ok = al(y, 16) && al(sh, 16) && al(h, 16) && al(out, 8);
+    if (pc->d % 4 == 0 && pc->topk <= RMDA_MAX_TOPK && pc->hc <= RMDA_MAX_HC && vec_ok) {
         if (out != nullptr) {
             hipLaunchKernelGGL(combine32_kernel<false>, dim3(pc->rows), dim3(256), 0, s, *pc, wt, slot, y, proj, sh,
                                inj, h, out);

@@ -254,3 +254,21 @@ def test_layer_nonfinite_tokens(ctx):
     assert np.isfinite(got[ok]).all()
     max_abs, rel = out_metrics(got[ok], ref["out"][ok])
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_layer_rejects_misaligned_pointers():
+    """x one fp16 element past 16-byte alignment: RMDA_ERR_ARG (-1) before
+    anything is enqueued (the kernels read 16-byte chunks of x rows)."""
+    c = api.Context(0)
+    inp = inputs.make_inputs(c, configs.CONFIGS[1], seed=0)
+    shape = inp["shape"]
+    x = inp["x"]
+    xbuf = torch.empty(x.numel() + 8, dtype=torch.float16, device="cuda")
+    xm = xbuf[1:1 + x.numel()].view_as(x)
+    assert xm.data_ptr() % 16 != 0
+    out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
+    with pytest.raises(api.MoeError) as e:
+        c.layer(shape, xm, inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"], None, None, out,
+                inputs.workspace_for(shape))
+    assert e.value.code == -1
+    c.close()

@@ -397,3 +397,41 @@ def test_errors_are_sticky_and_reported(ctx):
         c.mm(100, 128, 32, 0xFFFFFFFF, 0xFFFFFFFF, p, p, p, None, idx)  # m % 128 != 0
     assert e.value.code == -2
     c.close()
+
+
+def test_misaligned_pointers(ctx):
+    """Entry points whose kernels need 16-byte rows reject other alignments
+    with RMDA_ERR_ARG (-1) and enqueue nothing; the drop-in combine falls
+    back to its per-element kernel and gives the same bits."""
+    c = api.Context(0)
+    raw = torch.zeros(4096 + 8, dtype=torch.float16, device="cuda")
+    with pytest.raises(api.MoeError) as e:
+        c.scatter_experts(8)
+        c.scatter(4, 2, 8, empty_u32(8), empty_u32(8), empty_u32(8), raw[1:513], raw[1:], empty_u32(8))
+    assert e.value.code == -1
+    c.clear_error()
+    with pytest.raises(api.MoeError) as e:
+        c.mm(128, 128, 32, 0xFFFFFFFF, 0xFFFFFFFF, raw[1:], raw[1:], torch.zeros(128 * 128 + 4, device="cuda")[1:],
+             None, empty_u32(1))
+    assert e.value.code == -1
+    c.clear_error()
+    c.close()
+    # combine: fp32 expert rows one float past 16-byte alignment take the
+    # per-element kernel; the output is checked against the oracle either way
+    r = rng(11)
+    rows, d, topk, E = 33, 256, 4, 16
+    p = r.standard_normal((rows, E)).astype(np.float32)
+    _, wt, _ = orc.route(p, E, topk)
+    slot = r.permutation(rows * topk).astype(np.uint32)
+    y = r.standard_normal((rows * topk, d)).astype(np.float32)
+    fields = (rows, d, topk, E, E, 8, 0, 0)
+    ref = orc.combine_plain(fields, wt, slot, y, p, None)
+    ybuf = torch.empty(rows * topk * d + 1, dtype=torch.float32, device="cuda")
+    for shift in (0, 1):
+        yd = ybuf[shift:shift + rows * topk * d]
+        yd.copy_(torch.from_numpy(y.reshape(-1)))
+        assert (yd.data_ptr() % 16 == 0) == (shift == 0)
+        out = torch.empty(rows, d, dtype=torch.float16, device="cuda")
+        ctx.combine_plain(fields, dev(wt), dev(slot), yd, dev(p), None, out)
+        ctx.sync()
+        np.testing.assert_allclose(f32(out), orc.h2f(orc.f2h(ref)), rtol=0, atol=2e-3)
