@@ -353,6 +353,7 @@ size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape);
  * fp16 (round to nearest even) on the way, in place of qwen_bf16; the router
  * matrix is copied exactly.  Enqueued on the context stream; `packed` must
  * hold rmda_moe_packed_bytes(shape) bytes and must not overlap the inputs.
+ * All pointers 16-byte aligned (RMDA_ERR_ARG otherwise).
  * A packed buffer is valid for contexts of the same library build. */
 int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const float *w_router,
                           const uint16_t *w_gate_up, const uint16_t *w_down, const uint16_t *w_sh_gate_up,

@@ -965,6 +965,10 @@ int rmda_moe_pack_weights(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
         (shape->shared > 0 && (w_sh_gate_up == nullptr || w_sh_down == nullptr))) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_pack_weights: null argument");
     }
+    if (!aligned(w_router, 16) || !aligned(w_gate_up, 16) || !aligned(w_down, 16) || !aligned(w_sh_gate_up, 16) ||
+        !aligned(w_sh_down, 16) || !aligned(packed, 16)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_pack_weights: weights and packed must be 16-byte aligned");
+    }
     char why[128];
     if (!check_shape(shape, why, sizeof(why))) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_pack_weights: %s", why);
