@@ -1480,13 +1480,21 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
     if (rc == RMDA_OK) {
         rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d);
     }
-    if (rc == RMDA_OK) {
-        const rmda_pc_qwen_elem_t pe{mrows, I, 2 * I, 0, I, 0, 1.0f};
-        rc = rmda_qwen_elem(c, &pe, scr<float>(q, p.g), scr<float>(q, p.hp));
-    }
+    // SwiGLU and the absmax of hp in one pass (the same values and the same
+    // slot value as qwen_elem then absmax), then the scaled cast
     uint32_t sh = RMDA_NO_SLOT;
     if (rc == RMDA_OK) {
-        rc = shim_cast(q, p, scr<float>(q, p.hp), scr<uint16_t>(q, p.hp16), mrows * I, &sh);
+        sh = shim_slot(q);
+        rc = sh == RMDA_NO_SLOT ? c->err : RMDA_OK;
+    }
+    if (rc == RMDA_OK) {
+        const rmda_pc_qwen_elem_t pe{mrows, I, 2 * I, 0, I, 0, 1.0f};
+        rc = hip_check(c, rmda_launch_elem_absmax(c->stream, &pe, scr<float>(q, p.g), scr<float>(q, p.hp), amax, sh),
+                       "moe_rec swiglu");
+    }
+    if (rc == RMDA_OK) {
+        const rmda_pc_cast_t pc{mrows * I, sh};
+        rc = rmda_cast_f16(c, &pc, scr<float>(q, p.hp), scr<uint16_t>(q, p.hp16), amax);
     }
     if (rc == RMDA_OK) {
         rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.hp16), sh, q->w_down, scr<float>(q, p.ye), mrows, d, I);

@@ -330,6 +330,10 @@ hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t 
 // elem.hip
 hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y);
 hipError_t rmda_launch_absmax(hipStream_t s, const rmda_pc_absmax_t *pc, const float *x, uint32_t *amax);
+// elem op 0 with the absmax of its output folded in (amax[slot] as
+// rmda_launch_absmax would leave it over y)
+hipError_t rmda_launch_elem_absmax(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y,
+                                   uint32_t *amax, uint32_t slot);
 hipError_t rmda_launch_cast(hipStream_t s, const rmda_pc_cast_t *pc, const float *src, uint16_t *dst,
                             const uint32_t *amax);
 hipError_t rmda_launch_bf16(hipStream_t s, uint32_t n, uint32_t *w);

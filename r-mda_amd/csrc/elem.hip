@@ -26,6 +26,39 @@ __global__ __launch_bounds__(256) void elem_kernel(rmda_pc_qwen_elem_t pc, const
     }
 }
 
+// elem op 0 (SwiGLU) and the absmax of its output in one pass, for the
+// qwen.c recording, where the absmax pass re-read all of y: y is the same
+// expression per element as elem_kernel's, and amax[slot] the same fmaxf of
+// fabsf (NaN skipped) as absmax_kernel's, reduced per block and merged by
+// one atomicMax per block (a grid of at most 1024 blocks, as absmax's).
+__global__ __launch_bounds__(256) void elem_absmax_kernel(rmda_pc_qwen_elem_t pc, const float *__restrict__ a,
+                                                          float *__restrict__ y, uint32_t *__restrict__ amax,
+                                                          uint32_t slot) {
+    __shared__ float red[256];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t n = (uint64_t)pc.rows * pc.n;
+    float m = 0.0f;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + tid; i < n; i += (uint64_t)gridDim.x * 256) {
+        const uint32_t r = (uint32_t)(i / pc.n);
+        const uint32_t c = (uint32_t)(i % pc.n);
+        const float g = a[(size_t)r * pc.astride + pc.ao + c];
+        const float v = g / (1.0f + expf(-g)) * a[(size_t)r * pc.astride + pc.bo + c];
+        y[i] = v;
+        m = fmaxf(m, fabsf(v));
+    }
+    red[tid] = m;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (tid < s) {
+            red[tid] = fmaxf(red[tid], red[tid + s]);
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        atomicMax(&amax[slot], __builtin_bit_cast(uint32_t, red[0]));
+    }
+}
+
 __global__ __launch_bounds__(256) void absmax_kernel(const float *__restrict__ x, uint32_t n,
                                                      uint32_t *__restrict__ amax, uint32_t slot) {
     __shared__ float red[256];
@@ -114,6 +147,17 @@ hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const 
         return hipSuccess;
     }
     hipLaunchKernelGGL(elem_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, *pc, a, y);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_elem_absmax(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y,
+                                   uint32_t *amax, uint32_t slot) {
+    const uint64_t n = (uint64_t)pc->rows * pc->n;
+    if (n == 0) {
+        return hipSuccess;
+    }
+    const uint64_t blocks = (n + 255) / 256 > 1024 ? 1024 : (n + 255) / 256;
+    hipLaunchKernelGGL(elem_absmax_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, *pc, a, y, amax, slot);
     return hipGetLastError();
 }
 
