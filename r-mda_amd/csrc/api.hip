@@ -1508,13 +1508,22 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
             const rmda_pc_moe_mm_t pm{rows_pad, 2 * S, d, sx, RMDA_NO_SLOT};
             rc = rmda_moe_mm(c, &pm, scr<uint16_t>(q, p.a16), q->w_sh_gate_up, scr<float>(q, p.gs), amax, t1);
         }
-        if (rc == RMDA_OK) {
-            const rmda_pc_qwen_elem_t pe{rows, S, 2 * S, 0, S, 0, 1.0f};
-            rc = rmda_qwen_elem(c, &pe, scr<float>(q, p.gs), scr<float>(q, p.hs));
-        }
+        // SwiGLU with the absmax of hs folded in, then the scaled cast (as
+        // for the routed experts above)
         uint32_t ss = RMDA_NO_SLOT;
         if (rc == RMDA_OK) {
-            rc = shim_cast(q, p, scr<float>(q, p.hs), scr<uint16_t>(q, p.hs16), rows * S, &ss);
+            ss = shim_slot(q);
+            rc = ss == RMDA_NO_SLOT ? c->err : RMDA_OK;
+        }
+        if (rc == RMDA_OK) {
+            const rmda_pc_qwen_elem_t pe{rows, S, 2 * S, 0, S, 0, 1.0f};
+            rc = hip_check(c, rmda_launch_elem_absmax(c->stream, &pe, scr<float>(q, p.gs), scr<float>(q, p.hs), amax,
+                                                      ss),
+                           "moe_rec shared swiglu");
+        }
+        if (rc == RMDA_OK) {
+            const rmda_pc_cast_t pc{rows * S, ss};
+            rc = rmda_cast_f16(c, &pc, scr<float>(q, p.hs), scr<uint16_t>(q, p.hs16), amax);
         }
         if (rc == RMDA_OK) {
             const rmda_pc_moe_mm_t pm{rows_pad, d, S, ss, RMDA_NO_SLOT};
