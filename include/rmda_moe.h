@@ -141,6 +141,15 @@ typedef struct rmda_moe_ctx rmda_moe_ctx_t;
 int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream);
 void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx);
 int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream);
+/* Load buckets of the fused layer's grouped GEMMs (no counterpart in the
+ * reference, whose matmul_f16_moe has one 128 x 128 tile): an expert that
+ * receives at least `rows` rows in a call is hot, and when hot experts (and
+ * the shared expert, if it has that many rows) hold at least half of the
+ * call's rows, both GEMMs run the compute tile (256-row items, 8 waves of
+ * 128 x 64) instead of the weight-streaming tile (192-row items).  Either
+ * tile gives bitwise the same output.  Packed weights only; 0 disables the
+ * compute tile; the default is 256. */
+int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows);
 /* Sticky error: RMDA_OK or the first failure's code, with a message. */
 int rmda_moe_ctx_error(const rmda_moe_ctx_t *ctx);
 const char *rmda_moe_ctx_message(const rmda_moe_ctx_t *ctx);
@@ -313,6 +322,12 @@ typedef struct rmda_moe_ws_layout_t {
     size_t slot;
     size_t total;
     uint32_t proj_stride;
+    /* grouped-GEMM work list: items uint4 {group, first sorted row, rows, 0};
+     * n_items counts the weight-streaming tile's items (up to 192 rows),
+     * n_items_hot the compute tile's (up to 256 rows); one of the two is 0 */
+    size_t items;
+    size_t n_items;
+    size_t n_items_hot;
 } rmda_moe_ws_layout_t;
 
 size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape);

@@ -27,6 +27,12 @@ struct rmda_moe_ctx {
     uint32_t scatter_experts;
     // grouped-GEMM configuration (RMDA_MOE_GEMM_VARIANT overrides; tuning only)
     rmda_gemm2_cfg_t g2;
+    // compute tile for hot experts: rows that make an expert hot (0 = never
+    // use the tile) and its pipeline depth (RMDA_MOE_HOT_MIN and
+    // RMDA_MOE_HOT_STAGES override; tuning only)
+    uint32_t hot_min;
+    int hot_stages;
+    int hot_sched;
     // stage profiler: a ring of per-call event sets, harvested when full
     int prof_on;
     int prof_made;
@@ -126,7 +132,7 @@ int prof_mark(rmda_moe_ctx_t *c, uint32_t st) {
 }
 
 struct LayerPlan {
-    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, items, hp, ye, total;
+    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, ye, total;
     uint32_t ps, npairs, nblocks, max_items, sh_rows, sh_row0, groups_rows;
 };
 
@@ -190,6 +196,9 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.hist = take((size_t)p.nblocks * E * 4);
     p.done = take(4);
     p.n_items = take(4);
+    p.n_items_hot = take(4);
+    // one list serves both tiles: the hot tile's items (RMDA_GEMM_HOT_BM rows)
+    // are never more than the streaming tile's
     p.items = take((size_t)p.max_items * 16);
     p.hp = take((size_t)p.groups_rows * s->inter * 2);
     p.ye = take((size_t)p.groups_rows * s->d * 2);
@@ -276,6 +285,18 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
         c->g2 = rmda_gemm2_variant(atoi(v));
     }
     c->g2.grid = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 256u;
+    c->hot_min = RMDA_GEMM_HOT_MIN;
+    if (const char *v = getenv("RMDA_MOE_HOT_MIN")) {
+        c->hot_min = (uint32_t)strtoul(v, nullptr, 10);
+    }
+    c->hot_stages = 4;
+    if (const char *v = getenv("RMDA_MOE_HOT_STAGES")) {
+        c->hot_stages = atoi(v) == 5 ? 5 : 4;
+    }
+    c->hot_sched = 0;
+    if (const char *v = getenv("RMDA_MOE_HOT_SCHED")) {
+        c->hot_sched = atoi(v);
+    }
     if (prev >= 0 && prev != device) {
         (void)hipSetDevice(prev);
     }
@@ -367,6 +388,14 @@ int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream) {
         return RMDA_ERR_ARG;
     }
     ctx->stream = reinterpret_cast<hipStream_t>(stream);
+    return RMDA_OK;
+}
+
+int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows) {
+    if (ctx == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    ctx->hot_min = rows;
     return RMDA_OK;
 }
 
@@ -697,7 +726,27 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
     out->slot = p.slot;
     out->total = p.total;
     out->proj_stride = p.ps;
+    out->items = p.items;
+    out->n_items = p.n_items;
+    out->n_items_hot = p.n_items_hot;
     return RMDA_OK;
+}
+
+// One grouped GEMM of the fused layer over both load buckets: the compute
+// tile's launch (packed weights with the hot tile enabled) reads the hot
+// count, the streaming tile's reads the other; the rank kernel left one of
+// the two at zero.
+static int gemm_pair(rmda_moe_ctx_t *ctx, hipStream_t s, rmda_gemm_args_t g, rmda_gemm2_cfg_t cfg, bool packed,
+                     const uint32_t *n_items_hot, const char *what) {
+    if (packed && ctx->hot_min > 0) {
+        rmda_gemm_args_t h = g;
+        h.n_items = n_items_hot;
+        const int rc = hip_check(ctx, rmda_launch_gemm_hot(s, &h, cfg.grid, ctx->hot_stages, ctx->hot_sched), what);
+        if (rc != RMDA_OK) {
+            return rc;
+        }
+    }
+    return hip_check(ctx, rmda_launch_gemm2(s, &g, cfg, packed ? 1 : 0), what);
 }
 
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmda_moe_layer_args_t *args) {
@@ -806,6 +855,11 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.items = at<uint32_t>(ws, p.items);
         ra.n_items = at<uint32_t>(ws, p.n_items);
         ra.bm = RMDA_GEMM2_BM;
+        // load buckets: packed weights can take the compute tile when hot
+        // experts hold most rows (hot_min 0: never; the hot count is then 0)
+        ra.n_items_hot = at<uint32_t>(ws, p.n_items_hot);
+        ra.bm_hot = RMDA_GEMM_HOT_BM;
+        ra.hot_min = packed != nullptr ? ctx->hot_min : 0u;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.sh_row0;
         // all pairs in one rank block, or few enough pairs that every block
@@ -865,7 +919,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         if (gu.spec == 6 && (uint64_t)T * K >= 32ull * E) {
             gu.spec = 7;
         }
-        rc = hip_check(ctx, rmda_launch_gemm2(s, &g, gu, packed != nullptr), "layer gate_up");
+        // the compute tile first (it has work only when the rank kernel cut
+        // the list for it), then the streaming tile (work only otherwise)
+        rc = gemm_pair(ctx, s, g, gu, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), "layer gate_up");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_GATE_UP + 1);
@@ -884,7 +940,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.inter = 0;
         g.out = ye;
         g.ldo = d;
-        rc = hip_check(ctx, rmda_launch_gemm2(s, &g, ctx->g2, packed != nullptr), "layer down");
+        rc = gemm_pair(ctx, s, g, ctx->g2, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), "layer down");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_DOWN + 1);

@@ -203,6 +203,13 @@ struct rmda_rank_args_t {
     uint32_t *items;    // uint4 per item {expert, row0, rows, 0}
     uint32_t *n_items;  // one word
     uint32_t bm;        // rows per work item
+    // load-bucket tile choice (optional): when n_items_hot != NULL and the
+    // experts with >= hot_min rows hold at least half of all rows, the list
+    // is cut into bm_hot-row items counted in *n_items_hot (and *n_items = 0),
+    // else into bm-row items (and *n_items_hot = 0)
+    uint32_t *n_items_hot;
+    uint32_t bm_hot;
+    uint32_t hot_min;
     uint32_t shared_rows; // rows of the shared-expert group (0 = none)
     uint32_t shared_row0; // sorted-row base of the shared group
     // permutation written by the kernel itself when all pairs fit one rank
@@ -301,6 +308,15 @@ __host__ __device__ __forceinline__ size_t rmda_hp_index(uint32_t row, uint32_t 
     return ((size_t)(row / 16) * (inter / 32) + col / 32) * 512 + (row % 16) * 32 + col % 32;
 }
 rmda_gemm2_cfg_t rmda_gemm2_variant(int variant);
+// gemm_hot.hip: the compute tile for hot experts, over work items of up to
+// RMDA_GEMM_HOT_BM rows (packed weights only; same modes and bits as gemm2).
+// An expert is hot when it receives at least RMDA_GEMM_HOT_MIN rows.
+#define RMDA_GEMM_HOT_BM 256u
+#define RMDA_GEMM_HOT_MIN 256u
+static_assert(RMDA_GEMM_HOT_BM <= 16u * RMDA_ITEM_CLASSES && RMDA_GEMM_HOT_BM <= RMDA_ROWTOK_PAD,
+              "hot work items: row classes and the rowtok padding its gathers may read");
+// stages: LDS ring depth (4 or 5); sched: 0 = task_sched_t, 1 = chunk_sched_t
+hipError_t rmda_launch_gemm_hot(hipStream_t s, const rmda_gemm_args_t *a, uint32_t grid, int stages, int sched);
 hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm2_cfg_t c, int packed);
 // Reorder `groups` row-major [n_w][k] matrices (fp16, or bf16 when bf16_in)
 // into the packed slab order of K step bk (SWIGLU: gate/up interleave).

@@ -54,24 +54,14 @@
 //     gemm2_kernel on the same boxes: gate_up 175.3 -> 172.6 us, down
 //     106.1 -> 104.9 us (the second barrier helps gate_up, not down).
 #include "common.h"
+#include "gemm_sched.h"
 
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
+using namespace rmda_gemm;
 
 constexpr uint32_t BM = RMDA_GEMM2_BM;  // rows per work item (three 64-row blocks)
 constexpr uint32_t SLAB = 256;          // packed slab height (B rows) = the N tile
-
-// chunk swizzle of row r (BK/8 chunks per row): chunk c of row r sits in
-// slot c ^ ((r >> 1) & (BK/8 - 1)).  Chosen by measurement on gfx950
-// (SQ_LDS_BANK_CONFLICT over this kernel's exact fragment-read sequence):
-// zero conflict cycles for BK 32 and 64, where the unswizzled layout loses
-// 49% (BK 32) and 74% (BK 64) of LDS cycles to conflicts.  Depends only on
-// r mod 16, so it is the same for a slab row and a tile row.
-template <int BK>
-__device__ __forceinline__ uint32_t swz(uint32_t r) {
-    return (r >> 1) & (uint32_t)(BK / 8 - 1);
-}
 
 // B row of a group's weight matrix that slab row n of slab `slab` holds.
 // A SWIGLU slab is SLAB/64 groups of 32 gate rows followed by the 32
@@ -87,90 +77,6 @@ __device__ __forceinline__ uint32_t slab_row(uint32_t slab, uint32_t n, uint32_t
     }
     return slab * SLAB + n;
 }
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// all LDS reads of this wave done, then the workgroup barrier
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// wait until this wave's loads of the oldest pending stage have landed:
-// `after` later stages (0 .. 4) of L loads each may stay in flight
-template <int L>
-__device__ __forceinline__ void wait_after(uint32_t after) {
-    switch (after) {
-    case 0: wait_vm<0>(); break;
-    case 1: wait_vm<L>(); break;
-    case 2: wait_vm<2 * L>(); break;
-    case 3: wait_vm<3 * L>(); break;
-    default: wait_vm<4 * L>(); break;
-    }
-}
-
-// `loads` is one of the four per-wave stage sizes (uniform per wave)
-template <int LA, int LB_HI, int LB_LO>
-__device__ __forceinline__ void wait_stage(bool live, bool b_hi, uint32_t after) {
-    if (live) {
-        if (b_hi) {
-            wait_after<LA + LB_HI>(after);
-        } else {
-            wait_after<LA + LB_LO>(after);
-        }
-    } else {
-        if (b_hi) {
-            wait_after<LB_HI>(after);
-        } else {
-            wait_after<LB_LO>(after);
-        }
-    }
-}
-
-// Task schedule of a persistent launch: grid = 8 * S workgroups, workgroup b
-// on XCD b % 8.  The work list comes sorted by rows, largest first.
-//   * Item i goes to XCD snake(i / 8, i % 8, 8): the XCDs' shares balance,
-//     and the N tiles of one item (which share A rows) meet in one L2.
-//   * An XCD's tasks (its items in list order, N tiles innermost, so in
-//     falling cost) are dealt to its S workgroups round by round.  Rounds
-//     alternate direction so that pairs of rounds cancel; an odd number (>= 3)
-//     of full rounds starts with three rounds whose positions add up to
-//     3(S-1)/2 +- 1/2 for every workgroup.
-__device__ __forceinline__ uint32_t snake(uint32_t round, uint32_t pos, uint32_t width) {
-    return (round & 1u) != 0 ? width - 1u - pos : pos;
-}
-
-struct task_sched_t {
-    uint32_t xcd, wg, S, ntiles, full, ntask;
-    __device__ __forceinline__ task_sched_t(uint32_t n_items, uint32_t nt) {
-        xcd = blockIdx.x % 8u;
-        wg = blockIdx.x / 8u;
-        S = gridDim.x / 8u;
-        ntiles = nt;
-        const uint32_t rounds = n_items / 8u;
-        const uint32_t n_x = rounds + (snake(rounds, xcd, 8u) < n_items % 8u ? 1u : 0u);
-        const uint32_t total = n_x * nt;
-        full = total / S;
-        ntask = full + (pos(full) < total % S ? 1u : 0u);
-    }
-    // this workgroup's position in round q
-    __device__ __forceinline__ uint32_t pos(uint32_t q) const {
-        if (q < 3u && full >= 3u && (full & 1u) != 0 && (S & 1u) == 0) {
-            const uint32_t h = S / 2u;
-            return q == 0u ? wg : q == 1u ? (wg + h) % S : (wg < h ? S - 2u - 2u * wg : 2u * S - 1u - 2u * wg);
-        }
-        return snake(q, wg, S);
-    }
-    // work-list item of this workgroup's q-th task, and its N tile
-    __device__ __forceinline__ uint32_t item(uint32_t q, uint32_t &nt) const {
-        const uint32_t t = q * S + pos(q);
-        const uint32_t k = t / ntiles;
-        nt = t - k * ntiles;
-        return 8u * k + snake(k, xcd, 8u);
-    }
-};
 
 // Persistent workgroup: MB (=3) blocks of 64 rows x BN/64 (=4) column
 // blocks of 64, one wave each (12 waves).  Waves w and w + 4 share a SIMD, so
@@ -188,7 +94,6 @@ struct task_sched_t {
 // number of loads per stage (A rows of idle row blocks re-read row 0), and
 // the stores of a finished tile are never counted in a wait's allowance, so
 // each wait is exact or conservative.
-typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
 
 template <int MODE, int BN, int BK, int STAGES, bool PACKED, int BPOL>
 __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {

@@ -362,12 +362,63 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     if (a.items == nullptr) {
         return;
     }
+    // Tile choice by expert load: when the experts with at least hot_min rows
+    // (and the shared group, if it has that many) hold half the rows or more,
+    // the list is cut into bm_hot-row items for the compute tile and
+    // *n_items is 0; otherwise it is cut into bm-row items for the
+    // weight-streaming tile and *n_items_hot is 0.  Each GEMM kernel reads its
+    // own count, so the other one finds no work.
+    uint32_t bm = a.bm;
+    bool hot = false;
+    if (a.n_items_hot != nullptr) {
+        const uint32_t hm = a.hot_min;
+        uint32_t rows_all = 0;
+        uint32_t rows_hot = 0;
+        block_exscan(c0 + c1, sbuf, &rows_all);
+        block_exscan((c0 >= hm ? c0 : 0u) + (c1 >= hm ? c1 : 0u), sbuf, &rows_hot);
+        rows_all += a.shared_rows;
+        rows_hot += a.shared_rows >= hm ? a.shared_rows : 0u;
+        hot = hm > 0 && rows_hot > 0 && 2ull * rows_hot >= rows_all;
+        bm = hot ? a.bm_hot : a.bm;
+        if (tid == 0) {
+            *(hot ? a.n_items : a.n_items_hot) = 0u;
+        }
+    }
+    uint32_t *const n_out = hot ? a.n_items_hot : a.n_items;
+    if (hot) {
+        // The compute tile deals contiguous runs of tasks to each XCD, so its
+        // list is in expert order (an expert's items adjacent, the shared
+        // group last): the CUs of one XCD then work on the same expert's
+        // weight tiles at the same time and share them in their L2.
+        const uint32_t ni0 = (c0 + bm - 1u) / bm;
+        const uint32_t ni1 = (c1 + bm - 1u) / bm;
+        uint32_t n_routed = 0;
+        const uint32_t base0 = block_exscan(ni0 + ni1, sbuf, &n_routed);
+        uint4 *hitems = reinterpret_cast<uint4 *>(a.items);
+        for (uint32_t j = 0; j < 2; j += 1) {
+            const uint32_t c = j == 0 ? c0 : c1;
+            const uint32_t o = j == 0 ? o0 : o1;
+            const uint32_t b0 = j == 0 ? base0 : base0 + ni0;
+            const uint32_t ni = j == 0 ? ni0 : ni1;
+            for (uint32_t i = 0; i < ni; i += 1) {
+                hitems[b0 + i] = make_uint4(e0 + j, o + i * bm, min(bm, c - i * bm), 0u);
+            }
+        }
+        const uint32_t ns = (a.shared_rows + bm - 1u) / bm;
+        for (uint32_t i = tid; i < ns; i += NT) {
+            hitems[n_routed + i] = make_uint4(E, a.shared_row0 + i * bm, min(bm, a.shared_rows - i * bm), 0u);
+        }
+        if (tid == 0) {
+            *n_out = n_routed + ns;
+        }
+        return;
+    }
     // Grouped-GEMM work list: ceil(count/bm) items per expert plus the shared
     // group's, sorted by row count, largest first, in 16-row classes (the
     // GEMMs deal the list out in that order to balance their workgroups).
     // Each item takes a slot in its class with an LDS atomic, so the order
     // inside a class varies from run to run; an item's result does not.
-    const uint32_t ncls = (a.bm + 15u) / 16u;
+    const uint32_t ncls = (bm + 15u) / 16u;
     if (tid < RMDA_ITEM_CLASSES) {
         cls_n[tid] = 0;
     }
@@ -375,16 +426,16 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     uint32_t nfull[2], last_cls[2], slot_full[2], slot_last[2];
     for (uint32_t j = 0; j < 2; j += 1) {
         const uint32_t c = j == 0 ? c0 : c1;
-        const uint32_t ni = (c + a.bm - 1u) / a.bm;
+        const uint32_t ni = (c + bm - 1u) / bm;
         nfull[j] = ni > 0 ? ni - 1u : 0u;
-        last_cls[j] = ni > 0 ? (c - nfull[j] * a.bm + 15u) / 16u : 0u;
+        last_cls[j] = ni > 0 ? (c - nfull[j] * bm + 15u) / 16u : 0u;
         slot_full[j] = nfull[j] > 0 ? atomicAdd(&cls_n[ncls - 1u], nfull[j]) : 0u;
         slot_last[j] = ni > 0 ? atomicAdd(&cls_n[last_cls[j] - 1u], 1u) : 0u;
     }
-    const uint32_t ns = (a.shared_rows + a.bm - 1u) / a.bm;
+    const uint32_t ns = (a.shared_rows + bm - 1u) / bm;
     if (tid == 0 && ns > 0) {
         sh_slot[0] = ns > 1 ? atomicAdd(&cls_n[ncls - 1u], ns - 1u) : 0u;
-        sh_slot[1] = atomicAdd(&cls_n[(a.shared_rows - (ns - 1u) * a.bm + 15u) / 16u - 1u], 1u);
+        sh_slot[1] = atomicAdd(&cls_n[(a.shared_rows - (ns - 1u) * bm + 15u) / 16u - 1u], 1u);
     }
     __syncthreads();
     if (tid == 0) {
@@ -393,7 +444,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
             cls_b[c] = base;
             base += cls_n[c];
         }
-        *a.n_items = base;
+        *n_out = base;
     }
     __syncthreads();
     uint4 *items = reinterpret_cast<uint4 *>(a.items);
@@ -402,21 +453,21 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         const uint32_t c = j == 0 ? c0 : c1;
         const uint32_t o = j == 0 ? o0 : o1;
         for (uint32_t i = 0; i < nfull[j]; i += 1) {
-            items[cls_b[ncls - 1u] + slot_full[j] + i] = make_uint4(e, o + i * a.bm, a.bm, 0u);
+            items[cls_b[ncls - 1u] + slot_full[j] + i] = make_uint4(e, o + i * bm, bm, 0u);
         }
         if (last_cls[j] > 0) {
             const uint32_t i = nfull[j];
-            items[cls_b[last_cls[j] - 1u] + slot_last[j]] = make_uint4(e, o + i * a.bm, c - i * a.bm, 0u);
+            items[cls_b[last_cls[j] - 1u] + slot_last[j]] = make_uint4(e, o + i * bm, c - i * bm, 0u);
         }
     }
     if (ns > 0) {
         for (uint32_t i = tid; i + 1u < ns; i += NT) {
-            items[cls_b[ncls - 1u] + sh_slot[0] + i] = make_uint4(E, a.shared_row0 + i * a.bm, a.bm, 0u);
+            items[cls_b[ncls - 1u] + sh_slot[0] + i] = make_uint4(E, a.shared_row0 + i * bm, bm, 0u);
         }
         if (tid == 0) {
             const uint32_t i = ns - 1u;
-            const uint32_t rows = a.shared_rows - i * a.bm;
-            items[cls_b[(rows + 15u) / 16u - 1u] + sh_slot[1]] = make_uint4(E, a.shared_row0 + i * a.bm, rows, 0u);
+            const uint32_t rows = a.shared_rows - i * bm;
+            items[cls_b[(rows + 15u) / 16u - 1u] + sh_slot[1]] = make_uint4(E, a.shared_row0 + i * bm, rows, 0u);
         }
     }
 }

@@ -94,7 +94,8 @@ class StTensor(ctypes.Structure):
 class WsLayout(ctypes.Structure):
     _fields_ = [("proj", ctypes.c_size_t), ("idx", ctypes.c_size_t), ("wt", ctypes.c_size_t),
                 ("count", ctypes.c_size_t), ("off", ctypes.c_size_t), ("slot", ctypes.c_size_t),
-                ("total", ctypes.c_size_t), ("proj_stride", _u32)]
+                ("total", ctypes.c_size_t), ("proj_stride", _u32), ("items", ctypes.c_size_t),
+                ("n_items", ctypes.c_size_t), ("n_items_hot", ctypes.c_size_t)]
 
 
 class QwenMoe(ctypes.Structure):
@@ -116,6 +117,7 @@ SIGNATURES = {
     "rmda_moe_ctx_create": (ctypes.c_int, [ctypes.POINTER(_p), ctypes.c_int, _p]),
     "rmda_moe_ctx_destroy": (None, [_p]),
     "rmda_moe_set_stream": (ctypes.c_int, [_p, _p]),
+    "rmda_moe_set_hot_rows": (ctypes.c_int, [_p, _u32]),
     "rmda_moe_ctx_error": (ctypes.c_int, [_p]),
     "rmda_moe_ctx_message": (ctypes.c_char_p, [_p]),
     "rmda_moe_ctx_clear_error": (None, [_p]),

@@ -100,6 +100,11 @@ class Context:
     def set_stream(self, stream):
         self._check(self.L.rmda_moe_set_stream(self.h, self._raw_stream(stream)))
 
+    def set_hot_rows(self, rows):
+        """rmda_moe_set_hot_rows: rows that make an expert hot (0 = never use
+        the compute tile)."""
+        self._check(self.L.rmda_moe_set_hot_rows(self.h, int(rows)))
+
     def _check(self, rc):
         if rc != 0:
             msg = self.L.rmda_moe_ctx_message(self.h)
@@ -256,6 +261,8 @@ def ws_views(shape, workspace):
         "count": view(lay["count"], E, torch.int32),
         "off": view(lay["off"], E, torch.int32),
         "slot": view(lay["slot"], T * K, torch.int32),
+        "n_items": view(lay["n_items"], 1, torch.int32),
+        "n_items_hot": view(lay["n_items_hot"], 1, torch.int32),
     }
 
 
