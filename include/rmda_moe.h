@@ -346,6 +346,23 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
 int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
                    const rmda_moe_layer_args_t *args);
 
+/* Allocation-free variant of rmda_moe_layer.  It has no counterpart in the
+ * reference (whose recording always runs on caller-allocated scratch): it is
+ * for callers that cannot allocate, such as code under HIP graph capture or a
+ * serving loop that forbids hipMalloc.  Same arguments and results as
+ * rmda_moe_layer, except that args->workspace must be NULL and
+ * args->workspace_bytes 0: the workspace is the library's static device array
+ * of RMDA_STATIC_WS_BYTES, one per device, reserved when the code object is
+ * loaded and held until the process ends.  Shapes whose
+ * rmda_moe_workspace_bytes exceeds it fail with RMDA_ERR_CAPACITY (config 3,
+ * T=2048 x d=2048 x 128 experts top-8, needs 104.5 MB).  The call allocates
+ * nothing and enqueues only kernels (the rank ticket it needs zeroed is
+ * cleared by the router kernel).  Every call on a device shares that device's
+ * array and leaves its contents behind, so calls that overlap on one device
+ * (two streams, or two contexts, in flight at once) race. */
+#define RMDA_STATIC_WS_BYTES ((size_t)128 << 20)
+int rmda_moe_layer_static(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmda_moe_layer_args_t *args);
+
 /* ---- expert-weight packing (replaces the per-layer weight conversion at
  * upload, src/qwen.c:376-394: qwen_bf16 converts the bf16 expert weights to
  * fp16 in place after each layer's upload) ---- */

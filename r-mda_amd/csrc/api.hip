@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -20,7 +21,9 @@ struct rmda_moe_ctx {
     int err;
     char msg[256];
     // fixed scratch for rmda_moe_scatter (allocated once at creation)
-    uint32_t *scratch;
+    uint32_t *fixed_ws;
+    // this device's copy of the allocation-free layer's `scratch` array
+    void *static_ws;
     uint32_t *lrank;
     uint32_t *hist;
     uint32_t *done;
@@ -52,7 +55,18 @@ struct rmda_moe_ctx {
     int up_used[2];
 };
 
+// Workspace of the allocation-free layer (rmda_moe_layer_static): one copy
+// on every device the library runs on, held until the process ends.  Host
+// code never uses this name as an address: rmda_moe_ctx_create looks up the
+// device's copy with hipGetSymbolAddress (once per device) and every use goes
+// through that pointer.
+static __device__ __align__(256) uint8_t scratch[RMDA_STATIC_WS_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+void *g_static_ws[kMaxDevices];  // per device: the address of its `scratch`
 
 constexpr size_t kHistBlocks = (RMDA_CTX_MAX_PAIRS + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
 
@@ -266,18 +280,33 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
     c->err = RMDA_OK;
     c->msg[0] = 0;
     const size_t words = (size_t)RMDA_CTX_MAX_PAIRS + kHistBlocks * RMDA_MAX_EXPERTS + 64;
-    if (hipMalloc(&c->scratch, words * 4) != hipSuccess) {
+    if (hipMalloc(&c->fixed_ws, words * 4) != hipSuccess) {
         delete c;
         return RMDA_ERR_HIP;
     }
-    c->lrank = c->scratch;
+    c->lrank = c->fixed_ws;
     c->hist = c->lrank + RMDA_CTX_MAX_PAIRS;
     c->done = c->hist + kHistBlocks * RMDA_MAX_EXPERTS;
     // the rank ticket must start at zero; the kernel leaves it at zero
     if (hipMemset(c->done, 0, 64 * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-        (void)hipFree(c->scratch);
+        (void)hipFree(c->fixed_ws);
         delete c;
         return RMDA_ERR_HIP;
+    }
+    // this device's copy of the allocation-free layer's workspace, looked up
+    // once per device with the device current
+    if (device < kMaxDevices) {
+        std::lock_guard<std::mutex> lock(g_static_mu);
+        if (g_static_ws[device] == nullptr) {
+            void *ptr = nullptr;
+            if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+                (void)hipFree(c->fixed_ws);
+                delete c;
+                return RMDA_ERR_HIP;
+            }
+            g_static_ws[device] = ptr;
+        }
+        c->static_ws = g_static_ws[device];
     }
     c->scatter_experts = 0;
     c->g2 = rmda_gemm2_variant(0);
@@ -319,7 +348,7 @@ void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
         }
         (void)hipStreamDestroy(ctx->up_stream);
     }
-    (void)hipFree(ctx->scratch);
+    (void)hipFree(ctx->fixed_ws);
     if (ctx->prof_made) {
         for (uint32_t i = 0; i < RMDA_PROF_RING; i += 1) {
             for (uint32_t st = 0; st <= RMDA_PROF_STAGES; st += 1) {
@@ -960,6 +989,37 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ctx->prof_pending += 1;
     }
     return rc;
+}
+
+int rmda_moe_layer_static(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmda_moe_layer_args_t *args) {
+    int rc = enter(ctx);
+    if (rc != RMDA_OK) {
+        return rc;
+    }
+    if (shape == nullptr || args == nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer_static: null argument");
+    }
+    if (args->workspace != nullptr || args->workspace_bytes != 0) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer_static: takes no workspace (workspace must be NULL, "
+                    "workspace_bytes 0); the library's static scratch is used");
+    }
+    if (ctx->static_ws == nullptr) {
+        return fail(ctx, RMDA_ERR_DEVICE, "rmda_moe_layer_static: no static scratch on device %d", ctx->device);
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_layer_static: %s", why);
+    }
+    const size_t need = plan_layer(shape).total;
+    if (need > RMDA_STATIC_WS_BYTES) {
+        return fail(ctx, RMDA_ERR_CAPACITY, "rmda_moe_layer_static: this shape needs %zu bytes of workspace, "
+                    "beyond the static scratch's %zu (RMDA_STATIC_WS_BYTES); use rmda_moe_layer with a workspace",
+                    need, (size_t)RMDA_STATIC_WS_BYTES);
+    }
+    rmda_moe_layer_args_t a = *args;
+    a.workspace = ctx->static_ws;
+    a.workspace_bytes = RMDA_STATIC_WS_BYTES;
+    return rmda_moe_layer(ctx, shape, &a);
 }
 
 size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape) {

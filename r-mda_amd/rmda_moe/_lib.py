@@ -139,6 +139,7 @@ SIGNATURES = {
     "rmda_moe_workspace_layout": (ctypes.c_int, [_p, _p]),
     "rmda_moe_layer": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_packed_bytes": (ctypes.c_size_t, [_p]),
+    "rmda_moe_layer_static": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_pack_weights": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_int, _p]),
     "rmda_moe_prof_begin": (ctypes.c_int, [_p]),
     "rmda_moe_prof_end": (ctypes.c_int, [_p, _p, _p]),
