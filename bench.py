@@ -205,8 +205,9 @@ def measure_decode(ctx, torch, steps=100, warmup=50):
     res = {"workload": "decode: T=%d d=%d experts=%d top-%d inter=%d (BASELINE config 2)"
                        % (shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"]),
            "tokens/s": round(shape["rows"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 5), "steps": steps}
+    event_us = 1000.0 * ctx.prof_empty_ms() / max(n_prof, 1)
     for k in ("gate_up", "down"):
-        us = 1000.0 * stage_ms[k] / max(n_prof, 1)
+        us = 1000.0 * stage_ms[k] / max(n_prof, 1) - event_us
         gbs = work[k + "_bytes"] / (us * 1e-6) / 1e9
         res[k] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     del inp, ws, out, packed
@@ -425,7 +426,10 @@ def main():
     for _ in range(args.steps):
         step()
     stage_ms, n_prof = ctx.prof_end()
-    stage_us = {k: 1000.0 * v / max(n_prof, 1) for k, v in stage_ms.items()}
+    # per-stage GPU time net of what a stage boundary (one event) costs by
+    # itself; stages whose launch every call skipped are left out
+    event_us = 1000.0 * ctx.prof_empty_ms() / max(n_prof, 1)
+    stage_us = {k: 1000.0 * v / max(n_prof, 1) - event_us for k, v in stage_ms.items() if v > 0}
 
     views = api.ws_views(shape, ws)
     counts = views["count"].cpu().numpy()
@@ -474,6 +478,7 @@ def main():
             "ai_flop_per_byte": round(ai, 1), "ceiling_TFLOP/s": round(ceiling, 1),
             "frac_of_ceiling": round(gemm_tf / ceiling, 4), "experts_touched": touched}
     hbm_small = {"combine_GB/s": stages["combine"].get("GB/s")}
+    stages["event_interval_us"] = round(event_us, 2)
 
     if args.calib_copy:
         # a plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE

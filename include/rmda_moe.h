@@ -479,6 +479,13 @@ int rmda_moe_prof_begin(rmda_moe_ctx_t *ctx);
 /* Stop, wait for the stream, and return the summed milliseconds per stage
  * (ms[RMDA_PROF_STAGES]) and the number of layer calls they cover. */
 int rmda_moe_prof_end(rmda_moe_ctx_t *ctx, double *ms, uint32_t *layers);
+/* Summed length (ms) of an empty interval per profiled call since
+ * rmda_moe_prof_begin: two events recorded back to back on the stream, i.e.
+ * what one stage boundary costs by itself; subtract it from a stage's
+ * per-call average for the stage's own time.  A stage whose launch a call
+ * skipped (the top-k fused into the router, the permutation written by the
+ * rank kernel) adds no time and no event for that call. */
+int rmda_moe_prof_empty_ms(rmda_moe_ctx_t *ctx, double *ms);
 /* Name of stage i ("router", "route", ...), or NULL. */
 const char *rmda_moe_prof_stage_name(uint32_t i);
 

@@ -42,7 +42,12 @@ struct rmda_moe_ctx {
     uint32_t prof_pending;
     uint32_t prof_layers;
     double prof_ms[RMDA_PROF_STAGES];
-    hipEvent_t prof_ev[RMDA_PROF_RING][RMDA_PROF_STAGES + 1];
+    double prof_empty_ms;  // summed length of one empty interval per call
+    // per call: events opening the call and closing each stage, then one more
+    // recorded right after the opening one (an empty interval); a stage whose
+    // launch the call skipped records no event (bit st of prof_skip)
+    hipEvent_t prof_ev[RMDA_PROF_RING][RMDA_PROF_STAGES + 2];
+    uint32_t prof_skip[RMDA_PROF_RING];
     // weight upload: a stream of its own and two staging banks (pinned host +
     // device), created at the first upload
     int up_made;
@@ -52,6 +57,7 @@ struct rmda_moe_ctx {
     uint8_t *up_host[2];
     uint8_t *up_dev[2];
     hipEvent_t up_done[2];  // bank b's last upload (copy + pack) finished
+    hipEvent_t up_after;    // the compute stream's work queued before an upload's pack
     int up_used[2];
 };
 
@@ -125,11 +131,18 @@ int prof_harvest(rmda_moe_ctx_t *c) {
     int rc = hip_check(c, hipEventSynchronize(c->prof_ev[c->prof_pending - 1][RMDA_PROF_STAGES]),
                        "profiler hipEventSynchronize");
     for (uint32_t i = 0; i < c->prof_pending && rc == RMDA_OK; i += 1) {
+        float ms = 0.0f;
+        rc = hip_check(c, hipEventElapsedTime(&ms, c->prof_ev[i][0], c->prof_ev[i][RMDA_PROF_STAGES + 1]),
+                       "profiler hipEventElapsedTime");
+        c->prof_empty_ms += ms;
+        hipEvent_t prev = c->prof_ev[i][RMDA_PROF_STAGES + 1];
         for (uint32_t st = 0; st < RMDA_PROF_STAGES && rc == RMDA_OK; st += 1) {
-            float ms = 0.0f;
-            rc = hip_check(c, hipEventElapsedTime(&ms, c->prof_ev[i][st], c->prof_ev[i][st + 1]),
-                           "profiler hipEventElapsedTime");
+            if ((c->prof_skip[i] >> st) & 1u) {
+                continue;  // no launch, no event: the next stage's interval starts at `prev`
+            }
+            rc = hip_check(c, hipEventElapsedTime(&ms, prev, c->prof_ev[i][st + 1]), "profiler hipEventElapsedTime");
             c->prof_ms[st] += ms;
+            prev = c->prof_ev[i][st + 1];
         }
     }
     c->prof_layers += c->prof_pending;
@@ -137,12 +150,28 @@ int prof_harvest(rmda_moe_ctx_t *c) {
     return rc;
 }
 
-// Record the event that closes stage `st - 1` (st = 0 opens the call).
+// Record the event that closes stage `st - 1` (st = 0 opens the call and
+// records the empty interval right after).
 int prof_mark(rmda_moe_ctx_t *c, uint32_t st) {
     if (!c->prof_on) {
         return RMDA_OK;
     }
-    return hip_check(c, hipEventRecord(c->prof_ev[c->prof_pending][st], c->stream), "profiler hipEventRecord");
+    int rc = hip_check(c, hipEventRecord(c->prof_ev[c->prof_pending][st], c->stream), "profiler hipEventRecord");
+    if (st == 0) {
+        c->prof_skip[c->prof_pending] = 0;
+        if (rc == RMDA_OK) {
+            rc = hip_check(c, hipEventRecord(c->prof_ev[c->prof_pending][RMDA_PROF_STAGES + 1], c->stream),
+                           "profiler hipEventRecord");
+        }
+    }
+    return rc;
+}
+
+// Stage `st` launched nothing in this call: it records no event and adds no time.
+void prof_skip(rmda_moe_ctx_t *c, uint32_t st) {
+    if (c->prof_on) {
+        c->prof_skip[c->prof_pending] |= 1u << st;
+    }
 }
 
 struct LayerPlan {
@@ -346,6 +375,7 @@ void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
             (void)hipFree(ctx->up_dev[b]);
             (void)hipEventDestroy(ctx->up_done[b]);
         }
+        (void)hipEventDestroy(ctx->up_after);
         (void)hipStreamDestroy(ctx->up_stream);
     }
     (void)hipFree(ctx->fixed_ws);
@@ -366,7 +396,7 @@ int rmda_moe_prof_begin(rmda_moe_ctx_t *ctx) {
     }
     if (!ctx->prof_made) {
         for (uint32_t i = 0; i < RMDA_PROF_RING && rc == RMDA_OK; i += 1) {
-            for (uint32_t st = 0; st <= RMDA_PROF_STAGES && rc == RMDA_OK; st += 1) {
+            for (uint32_t st = 0; st <= RMDA_PROF_STAGES + 1 && rc == RMDA_OK; st += 1) {
                 rc = hip_check(ctx, hipEventCreate(&ctx->prof_ev[i][st]), "profiler hipEventCreate");
             }
         }
@@ -381,6 +411,15 @@ int rmda_moe_prof_begin(rmda_moe_ctx_t *ctx) {
     for (uint32_t st = 0; st < RMDA_PROF_STAGES; st += 1) {
         ctx->prof_ms[st] = 0.0;
     }
+    ctx->prof_empty_ms = 0.0;
+    return RMDA_OK;
+}
+
+int rmda_moe_prof_empty_ms(rmda_moe_ctx_t *ctx, double *ms) {
+    if (ctx == nullptr || ms == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    *ms = ctx->prof_empty_ms;
     return RMDA_OK;
 }
 
@@ -783,8 +822,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     if (rc != RMDA_OK) {
         return rc;
     }
-    if (shape == nullptr || args == nullptr || args->x == nullptr || args->w_router == nullptr ||
-        (args->packed == nullptr && (args->w_gate_up == nullptr || args->w_down == nullptr)) ||
+    if (shape == nullptr || args == nullptr || args->x == nullptr ||
+        (args->packed == nullptr && (args->w_router == nullptr || args->w_gate_up == nullptr ||
+                                     args->w_down == nullptr)) ||
         (args->out == nullptr && args->h == nullptr) || args->workspace == nullptr) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: null argument");
     }
@@ -864,9 +904,11 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     // A1 top-k (unless fused above)
     if (rc == RMDA_OK && !fuse_route) {
         rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
-    }
-    if (rc == RMDA_OK) {
-        rc = prof_mark(ctx, RMDA_STAGE_ROUTE + 1);
+        if (rc == RMDA_OK) {
+            rc = prof_mark(ctx, RMDA_STAGE_ROUTE + 1);
+        }
+    } else if (rc == RMDA_OK) {
+        prof_skip(ctx, RMDA_STAGE_ROUTE);
     }
     // A2 counts, offsets, block bases and the GEMM work list
     bool self_perm = false;
@@ -912,9 +954,11 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
                        rmda_launch_permute(s, idx, lrank, at<uint32_t>(ws, p.hist), p.npairs, K, E, slot, rowtok,
                                            nullptr, nullptr, 0),
                        "layer permute");
-    }
-    if (rc == RMDA_OK) {
-        rc = prof_mark(ctx, RMDA_STAGE_PERMUTE + 1);
+        if (rc == RMDA_OK) {
+            rc = prof_mark(ctx, RMDA_STAGE_PERMUTE + 1);
+        }
+    } else if (rc == RMDA_OK) {
+        prof_skip(ctx, RMDA_STAGE_PERMUTE);
     }
     rmda_gemm_args_t g{};
     g.items = at<uint32_t>(ws, p.items);
@@ -1179,6 +1223,9 @@ int up_reserve(rmda_moe_ctx_t *ctx, size_t bytes) {
         for (int b = 0; rc == RMDA_OK && b < 2; b += 1) {
             rc = hip_check(ctx, hipEventCreateWithFlags(&ctx->up_done[b], hipEventDisableTiming), "upload event");
         }
+        if (rc == RMDA_OK) {
+            rc = hip_check(ctx, hipEventCreateWithFlags(&ctx->up_after, hipEventDisableTiming), "upload event");
+        }
         if (rc != RMDA_OK) {
             return rc;
         }
@@ -1303,6 +1350,15 @@ int rmda_moe_upload_layer(rmda_moe_ctx_t *ctx, const rmda_st_t *st, const char *
     up_copy(host, pieces);
     hipStream_t us = ctx->up_stream;
     rc = hip_check(ctx, hipMemcpyAsync(dev, host, total, hipMemcpyHostToDevice, us), "upload copy");
+    // `packed` may still be read by layers already queued on the compute
+    // stream (a rotation that reuses packed buffers): the pack kernels that
+    // overwrite it wait for that work; the copy above does not need to
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, hipEventRecord(ctx->up_after, ctx->stream), "upload event");
+    }
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, hipStreamWaitEvent(us, ctx->up_after, 0), "upload wait for queued layers");
+    }
     if (rc == RMDA_OK) {
         rc = pack_layer(ctx, us, shape, reinterpret_cast<const float *>(dev + off_r),
                         reinterpret_cast<const uint16_t *>(dev + off_gu), tgu.dtype == RMDA_ST_BF16,

@@ -205,11 +205,12 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         }
         __syncthreads();
     }
-    // Hand-off: the last block to arrive finalises.  The block totals are
-    // stored and later read with device-scope atomics, and each store has
-    // completed (vmcnt(0)) before the block takes its ticket, so the last
-    // block sees every total without a device-scope fence: on this multi-XCD
-    // part such a fence writes back and invalidates the whole L2.
+    // Hand-off: the last block to arrive finalises.  Every wave stores its
+    // share of the block totals with device-scope atomic stores and waits for
+    // them (vmcnt(0)) before the workgroup barrier; thread 0 then takes the
+    // ticket with a device-scope acquire-release increment, which releases
+    // the block's totals to the last block and, in the last block, acquires
+    // all of them before its device-scope loads read them.
     // A single block needs no hand-off: its own counts (run[]) are the totals.
     if (all) {
         count_add(tid);
@@ -233,8 +234,8 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
-            // atomicInc wraps the ticket back to 0 on the last block
-            s_last = atomicInc(a.done, nb - 1) == nb - 1;
+            // the increment wraps the ticket back to 0 on the last block
+            s_last = __builtin_amdgcn_atomic_inc32(a.done, nb - 1, __ATOMIC_ACQ_REL, "agent") == nb - 1;
         }
         __syncthreads();
         if (!s_last) {

@@ -143,6 +143,7 @@ SIGNATURES = {
     "rmda_moe_pack_weights": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, ctypes.c_int, _p]),
     "rmda_moe_prof_begin": (ctypes.c_int, [_p]),
     "rmda_moe_prof_end": (ctypes.c_int, [_p, _p, _p]),
+    "rmda_moe_prof_empty_ms": (ctypes.c_int, [_p, _p]),
     "rmda_moe_prof_stage_name": (ctypes.c_char_p, [_u32]),
     "rmda_moe_fill_normal_f16": (ctypes.c_int, [_p, _p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
                                                 ctypes.c_float]),

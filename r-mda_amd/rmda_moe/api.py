@@ -245,6 +245,12 @@ class Context:
         names = [self.L.rmda_moe_prof_stage_name(i).decode() for i in range(_lib.PROF_STAGES)]
         return dict(zip(names, list(ms))), n.value
 
+    def prof_empty_ms(self):
+        """rmda_moe_prof_empty_ms: summed empty-interval time of the last profiled run."""
+        ms = ctypes.c_double()
+        self._check(self.L.rmda_moe_prof_empty_ms(self.h, ctypes.byref(ms)))
+        return ms.value
+
     def fill_normal(self, t, stream, seed, std):
         if t.dtype == torch.float16:
             self._check(self.L.rmda_moe_fill_normal_f16(self.h, _ptr(t), t.numel(), stream, seed, std))

@@ -3,10 +3,8 @@ benchmark configuration.
 
 Routing intermediates are bit-exact (router logits, expert indices, counts,
 offsets, slots); the fp16 output is within max-abs 2e-3 and relative L2 1e-3
-of the oracle's fp32 output.  Configurations 1 and 2 are checked on every
-token; 3-5 on every token's routing and on a seeded sample of output rows
-(the oracle computes only those rows' expert FFNs; each output row depends
-only on its own token, so the sample is exact, not approximate).
+of the oracle's fp32 output, on every output row (the oracle's layer runs
+multithreaded), so every (work item, 16-row group) of both GEMMs is covered.
 """
 import numpy as np
 import pytest
@@ -54,7 +52,7 @@ def check_layer(ctx, cfg, seed, n_sample=None):
     sel = None
     if n_sample is not None and n_sample < T:
         sel = np.sort(np.random.default_rng(seed).choice(T, n_sample, replace=False)).astype(np.uint32)
-    ref = orc.layer(host, tile=16, rows_sel=sel)
+    ref = orc.layer(host, tile=16, rows_sel=sel, threads=16)
     assert np.array_equal(views["proj"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
     assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
     assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
@@ -84,8 +82,14 @@ def test_layer_full(ctx, cfg_id):
 
 
 @pytest.mark.parametrize("cfg_id", [3, 4, 5])
-def test_layer_sampled(ctx, cfg_id):
-    check_layer(ctx, configs.CONFIGS[cfg_id], seed=0, n_sample=48)
+def test_layer_all_rows(ctx, cfg_id):
+    check_layer(ctx, configs.CONFIGS[cfg_id], seed=0)
+
+
+# The reference teacher's own MoE shape (src/qwen.c:11-37, src/qwen.h:20-21):
+# hidden 2560, 512 experts, top-10, expert and shared width 640, at a row
+# chunk of 256 tokens
+TEACHER = dict(name="teacher", rows=256, d=2560, experts=512, topk=10, inter=640, shared=640, skew=False)
 
 
 @pytest.mark.parametrize("cfg", [
@@ -99,7 +103,11 @@ def test_layer_sampled(ctx, cfg_id):
     dict(name="skew_k1", rows=900, d=512, experts=24, topk=1, inter=256, shared=256, skew=True),
     # maximum top-k, 512 experts, d not a multiple of 512 (1280 = 5 x 256: 10 sub-tiles per router chunk)
     dict(name="e512_k16", rows=33, d=1280, experts=512, topk=16, inter=128, shared=0, skew=False),
-])
+    # 3081 pairs: several rank blocks that all count every pair (count_all), a
+    # partial last block and npairs % 4 = 1 pairs past the 16-byte words
+    dict(name="count_all_tail", rows=1027, d=256, experts=40, topk=3, inter=128, shared=0, skew=False),
+    TEACHER,
+], ids=lambda c: c["name"])
 def test_layer_more_shapes(ctx, cfg):
     """Shapes away from the benchmark configurations, through both weight
     layouts, against the oracle: routing bit-exact, output within tolerance,
@@ -116,9 +124,9 @@ def test_layer_more_shapes(ctx, cfg):
     dict(name="large_skew_shared", rows=32768, d=512, experts=64, topk=2, inter=256, shared=256, skew=True),
 ])
 def test_layer_large(ctx, cfg):
-    """Sizes far above the benchmark configurations: routing bit-exact on
-    every token, output within tolerance on a sample of rows."""
-    check_layer(ctx, cfg, seed=7, n_sample=32)
+    """Sizes far above the benchmark configurations: routing bit-exact and
+    output within tolerance on every token."""
+    check_layer(ctx, cfg, seed=7)
 
 
 def test_layer_other_seed_and_ragged(ctx):
@@ -128,16 +136,20 @@ def test_layer_other_seed_and_ragged(ctx):
     check_layer(ctx, cfg, seed=1)
 
 
-@pytest.mark.parametrize("cfg_id,n_sample", [(1, None), (5, 16)])
-def test_layer_hyper_connection_epilogue(ctx, cfg_id, n_sample):
+@pytest.mark.parametrize("cfg,n_sample,hc,inj_stride,inj_off", [
+    (configs.CONFIGS[1], None, 4, 11, 3),
+    (configs.CONFIGS[5], 16, 4, 11, 3),
+    # the teacher's streams: 4 of them, injection logits at hc_rank 320 of a
+    # row padded to MDA_QWEN_HC_PAD 384 (src/qwen.h:20-21)
+    (TEACHER, None, 4, 384, 320),
+], ids=["tiny", "fine_shared", "teacher"])
+def test_layer_hyper_connection_epilogue(ctx, cfg, n_sample, hc, inj_stride, inj_off):
     """h[r][s][c] += y[r][c] * 2 * sigmoid(inj[r*stride + off + s] / hc)
     (shader/moe_combine.comp:36-38), with y the fp32 layer output: checked
     against the oracle's fp32 output in float64; `out` may be omitted."""
-    cfg = configs.CONFIGS[cfg_id]
     inp = inputs.make_inputs(ctx, cfg, seed=4)
     shape = inp["shape"]
     T, d = shape["rows"], shape["d"]
-    hc, inj_stride, inj_off = 4, 11, 3
     g = torch.Generator(device="cuda").manual_seed(9)
     h0 = torch.randn(T, hc, d, device="cuda", generator=g)
     inj = torch.randn(T, inj_stride, device="cuda", generator=g) * 3
@@ -152,7 +164,7 @@ def test_layer_hyper_connection_epilogue(ctx, cfg_id, n_sample):
     sel = None
     if n_sample:
         sel = np.sort(np.random.default_rng(2).choice(T, n_sample, replace=False)).astype(np.uint32)
-    ref = orc.layer(host, tile=16, rows_sel=sel)
+    ref = orc.layer(host, tile=16, rows_sel=sel, threads=16)
     rows = np.arange(T) if sel is None else sel.astype(np.int64)
     gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[rows, inj_off:inj_off + hc] / hc))
     want = h0.cpu().numpy()[rows].astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]

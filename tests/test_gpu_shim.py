@@ -23,6 +23,8 @@ SHAPES = [
     configs.CONFIGS[2],  # decode: 128 experts, top-8, T = 128
     dict(name="shared_small", rows=200, d=256, experts=16, topk=4, inter=128, shared=128, skew=False),
     dict(name="ragged_k5", rows=77, d=512, experts=24, topk=5, inter=256, shared=0, skew=False),
+    # the reference teacher's own MoE shape (src/qwen.c:11-37), a 256-row chunk
+    dict(name="teacher", rows=256, d=2560, experts=512, topk=10, inter=640, shared=640, skew=False),
 ]
 
 
@@ -49,7 +51,7 @@ def test_moe_rec_matches_oracle_reference_mode(ctx, cfg):
     out = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
     q.moe_rec(inp["x"].float(), T, out=out)
     ctx.sync()
-    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1)
+    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1, threads=16)
     v = q.views(T)
     assert np.array_equal(v["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
     assert np.array_equal(u32(v["idx"]), ref["idx"]), "expert indices"
@@ -65,13 +67,18 @@ def test_moe_rec_matches_oracle_reference_mode(ctx, cfg):
     assert q.q.n_slots == (3 if cfg["shared"] else 2)
 
 
-def test_moe_rec_hyper_connection_streams(ctx):
+@pytest.mark.parametrize("cfg,hc,stride,rank", [
+    (dict(name="hc", rows=96, d=256, experts=12, topk=3, inter=128, shared=128, skew=False), 4, 10, 3),
+    # the teacher: 4 streams, injection logits at hc_rank 320 of rows padded to
+    # MDA_QWEN_HC_PAD 384 (src/qwen.c:13-28, src/qwen.h:20-21)
+    (dict(name="teacher", rows=128, d=2560, experts=512, topk=10, inter=640, shared=640, skew=False), 4, 384, 320),
+], ids=["small", "teacher"])
+def test_moe_rec_hyper_connection_streams(ctx, cfg, hc, stride, rank):
     """h[r, s, c] += y[r, c] * 2 * sigmoid(inj[r, hc_rank + s] / hc), the
     reference's combine epilogue (shader/moe_combine.comp:36-38), against the
     oracle's y; the plain output of the same call is the y the streams got."""
-    cfg = dict(name="hc", rows=96, d=256, experts=12, topk=3, inter=128, shared=128, skew=False)
     inp = inputs.make_inputs(ctx, cfg, seed=5)
-    T, d, hc, stride, rank = cfg["rows"], cfg["d"], 4, 10, 3
+    T, d = cfg["rows"], cfg["d"]
     q = make_shim(ctx, inp, hc=hc, hc_rank=rank, inj_stride=stride)
     g = torch.Generator(device="cuda").manual_seed(9)
     h0 = torch.randn(T, hc, d, device="cuda", generator=g)
@@ -80,7 +87,7 @@ def test_moe_rec_hyper_connection_streams(ctx):
     out = torch.empty(T, d, dtype=torch.float16, device="cuda")
     q.moe_rec(inp["x"].float(), T, inj=inj, h=h, out=out)
     ctx.sync()
-    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1)
+    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1, threads=16)
     gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[:, rank:rank + hc] / hc))
     want = h0.cpu().numpy().astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]
     err = np.abs(h.cpu().numpy().astype(np.float64) - want).max()

@@ -376,6 +376,29 @@ def test_elem_absmax_cast_bf16(ctx):
     assert np.array_equal(u32(wd), refw)
 
 
+def test_qwen_bf16_every_bit_pattern(ctx):
+    """qwen_bf16 over all 65536 bf16 values in both halves of the word:
+    overflow to inf, fp16 subnormals, values that flush to zero, both zeros,
+    infinities and NaNs.  Every non-NaN result is bitwise the oracle's; a NaN
+    stays a NaN of the same sign."""
+    lo = np.arange(65536, dtype=np.uint32)
+    hi = rng(29).permutation(lo)
+    w = (hi << np.uint32(16)) | lo
+    refw = orc.qwen_bf16(w)
+    wd = dev(w)
+    ctx.qwen_bf16(w.size, wd)
+    ctx.sync()
+    got = u32(wd)
+    for shift in (0, 16):
+        g = ((got >> np.uint32(shift)) & np.uint32(0xFFFF)).astype(np.uint16)
+        e = ((refw >> np.uint32(shift)) & np.uint32(0xFFFF)).astype(np.uint16)
+        nan = ((e & 0x7C00) == 0x7C00) & ((e & 0x03FF) != 0)
+        assert np.array_equal(g[~nan], e[~nan]), "non-NaN bf16 -> fp16 differs"
+        gnan = ((g & 0x7C00) == 0x7C00) & ((g & 0x03FF) != 0)
+        assert gnan[nan].all() and np.array_equal(g[nan] >> 15, e[nan] >> 15), "NaN not kept"
+        print("  half %d: %d NaN payloads equal of %d" % (shift // 16, int((g[nan] == e[nan]).sum()), int(nan.sum())))
+
+
 # ---------------------------------------------------------------- error behaviour
 
 def test_errors_are_sticky_and_reported(ctx):

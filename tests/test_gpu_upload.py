@@ -93,6 +93,45 @@ def test_layer_on_uploaded_weights(ctx, tmp_path):
     assert torch.equal(out_up.view(torch.int16), out_hf.view(torch.int16))
 
 
+def test_upload_into_buffer_in_use(ctx, tmp_path):
+    """A rotation that reuses a packed buffer: layers reading buffer P are
+    queued on the compute stream, then layer B's weights are uploaded into P
+    at once.  The pack kernels that overwrite P wait for the queued layers, so
+    every queued call still sees A's weights, and a layer after
+    rmda_moe_upload_wait sees B's."""
+    shape = dict(shapes()[0], rows=64)
+    cfg = dict(configs.CONFIGS[1], **shape, name="reuse")
+    inp = inputs.make_inputs(ctx, cfg, seed=4)
+    rng = np.random.default_rng(9)
+    ta = st.moe_layer_tensors(PREFIX % 0, shape, rng, dtype="F16")
+    tb = st.moe_layer_tensors(PREFIX % 1, shape, rng, dtype="F16")
+    path = tmp_path / "w.safetensors"
+    st.write(str(path), {**ta, **tb})
+    ws = inputs.workspace_for(shape)
+    outs = [torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda") for _ in range(3)]
+    with st.SafeTensors(str(path)) as f:
+        packed = ctx.upload_layer(f, PREFIX % 0, shape)
+        ctx.upload_wait()
+        ref_a = torch.empty_like(outs[0])
+        ctx.layer(shape, inp["x"], None, None, None, None, None, None, ref_a, ws, packed=packed)
+        pb = ctx.upload_layer(f, PREFIX % 1, shape)
+        ctx.upload_wait()
+        ref_b = torch.empty_like(outs[0])
+        ctx.layer(shape, inp["x"], None, None, None, None, None, None, ref_b, ws, packed=pb)
+        ctx.sync()
+        assert not torch.equal(ref_a.view(torch.int16), ref_b.view(torch.int16))
+        # many queued calls on P (several ms of work), the last one into outs[0]
+        for _ in range(400):
+            ctx.layer(shape, inp["x"], None, None, None, None, None, None, outs[1], ws, packed=packed)
+        ctx.layer(shape, inp["x"], None, None, None, None, None, None, outs[0], ws, packed=packed)
+        ctx.upload_layer(f, PREFIX % 1, shape, packed=packed)
+        ctx.upload_wait()
+        ctx.layer(shape, inp["x"], None, None, None, None, None, None, outs[2], ws, packed=packed)
+        ctx.sync()
+    assert torch.equal(outs[0].view(torch.int16), ref_a.view(torch.int16)), "a queued layer saw the new weights"
+    assert torch.equal(outs[2].view(torch.int16), ref_b.view(torch.int16)), "the layer after the wait saw old weights"
+
+
 def test_upload_errors(ctx, tmp_path):
     shape = shapes()[0]
     rng = np.random.default_rng(7)
