@@ -150,6 +150,24 @@ int rmda_moe_set_stream(rmda_moe_ctx_t *ctx, void *stream);
  * tile gives bitwise the same output.  Packed weights only; 0 disables the
  * compute tile; the default is 256. */
 int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows);
+/* Which grouped-GEMM tile launches (no counterpart in the reference).  The
+ * choice is made on the device, from the call's routing, after the host has
+ * enqueued the GEMM launches, so:
+ *   RMDA_TILE_AUTO      launches both tiles every call; the one whose list
+ *                       the rank kernel left empty exits at once (about
+ *                       4 us per launch on MI355X);
+ *   RMDA_TILE_ADAPTIVE  (default) launches only the tile the context's
+ *                       previous call chose (the rank kernel reports its
+ *                       choice to a host-visible word) and makes the rank
+ *                       kernel cut its list for that tile; the first call,
+ *                       and the first after rmda_moe_set_hot_rows or this
+ *                       function, runs as AUTO;
+ *   RMDA_TILE_STREAM / RMDA_TILE_HOT  always that tile.
+ * Every policy gives bitwise the same output; calls with rows < hot rows
+ * (no expert can be hot) and HF-layout weights launch the streaming tile
+ * only. */
+enum { RMDA_TILE_ADAPTIVE = 0, RMDA_TILE_AUTO = 1, RMDA_TILE_STREAM = 2, RMDA_TILE_HOT = 3 };
+int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy);
 /* Sticky error: RMDA_OK or the first failure's code, with a message. */
 int rmda_moe_ctx_error(const rmda_moe_ctx_t *ctx);
 const char *rmda_moe_ctx_message(const rmda_moe_ctx_t *ctx);

@@ -36,6 +36,12 @@ struct rmda_moe_ctx {
     uint32_t hot_min;
     int hot_stages;
     int hot_sched;
+    // tile policy (RMDA_TILE_*; RMDA_MOE_TILE_POLICY overrides, tuning only)
+    // and the word the rank kernel reports its tile choice to (pinned host
+    // memory, mapped into the device)
+    int tile_policy;
+    uint32_t *tile_hint_host;
+    uint32_t *tile_hint_dev;
     // stage profiler: a ring of per-call event sets, harvested when full
     int prof_on;
     int prof_made;
@@ -355,6 +361,18 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
     if (const char *v = getenv("RMDA_MOE_HOT_SCHED")) {
         c->hot_sched = atoi(v);
     }
+    c->tile_policy = RMDA_TILE_ADAPTIVE;
+    if (const char *v = getenv("RMDA_MOE_TILE_POLICY")) {  // tuning only
+        const int pol = atoi(v);
+        c->tile_policy = pol >= RMDA_TILE_ADAPTIVE && pol <= RMDA_TILE_HOT ? pol : RMDA_TILE_ADAPTIVE;
+    }
+    if (hipHostMalloc(reinterpret_cast<void **>(&c->tile_hint_host), 64, hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void **>(&c->tile_hint_dev), c->tile_hint_host, 0) != hipSuccess) {
+        (void)hipFree(c->fixed_ws);
+        delete c;
+        return RMDA_ERR_HIP;
+    }
+    __atomic_store_n(c->tile_hint_host, 0u, __ATOMIC_RELAXED);
     if (prev >= 0 && prev != device) {
         (void)hipSetDevice(prev);
     }
@@ -379,6 +397,7 @@ void rmda_moe_ctx_destroy(rmda_moe_ctx_t *ctx) {
         (void)hipStreamDestroy(ctx->up_stream);
     }
     (void)hipFree(ctx->fixed_ws);
+    (void)hipHostFree(ctx->tile_hint_host);
     if (ctx->prof_made) {
         for (uint32_t i = 0; i < RMDA_PROF_RING; i += 1) {
             for (uint32_t st = 0; st <= RMDA_PROF_STAGES; st += 1) {
@@ -464,6 +483,16 @@ int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows) {
         return RMDA_ERR_ARG;
     }
     ctx->hot_min = rows;
+    __atomic_store_n(ctx->tile_hint_host, 0u, __ATOMIC_RELAXED);  // the next call chooses afresh
+    return RMDA_OK;
+}
+
+int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy) {
+    if (ctx == nullptr || policy < RMDA_TILE_ADAPTIVE || policy > RMDA_TILE_HOT) {
+        return RMDA_ERR_ARG;
+    }
+    ctx->tile_policy = policy;
+    __atomic_store_n(ctx->tile_hint_host, 0u, __ATOMIC_RELAXED);
     return RMDA_OK;
 }
 
@@ -800,17 +829,17 @@ int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_
     return RMDA_OK;
 }
 
-// One grouped GEMM of the fused layer over both load buckets: the compute
-// tile's launch (packed weights with the hot tile enabled) reads the hot
-// count, the streaming tile's reads the other; the rank kernel left one of
-// the two at zero.
+// One grouped GEMM of the fused layer over the load buckets: the compute
+// tile's launch reads the hot count, the streaming tile's the other (the rank
+// kernel left one of the two at zero); tile_mode 1 or 2 launches only the
+// tile the rank kernel was told to cut its list for.
 static int gemm_pair(rmda_moe_ctx_t *ctx, hipStream_t s, rmda_gemm_args_t g, rmda_gemm2_cfg_t cfg, bool packed,
-                     const uint32_t *n_items_hot, const char *what) {
-    if (packed && ctx->hot_min > 0) {
+                     const uint32_t *n_items_hot, uint32_t tile_mode, const char *what) {
+    if (tile_mode != 1u) {
         rmda_gemm_args_t h = g;
         h.n_items = n_items_hot;
         const int rc = hip_check(ctx, rmda_launch_gemm_hot(s, &h, cfg.grid, ctx->hot_stages, ctx->hot_sched), what);
-        if (rc != RMDA_OK) {
+        if (rc != RMDA_OK || tile_mode == 2u) {
             return rc;
         }
     }
@@ -910,6 +939,22 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     } else if (rc == RMDA_OK) {
         prof_skip(ctx, RMDA_STAGE_ROUTE);
     }
+    // Tile of the two GEMMs (0: both launch, the rank kernel decides; 1: the
+    // streaming tile only; 2: the compute tile only).  No expert can be hot
+    // with fewer rows than hot_min (a token adds at most one row per expert).
+    const bool hot_possible = packed != nullptr && ctx->hot_min > 0 && T >= ctx->hot_min;
+    uint32_t tile_mode = 1;
+    if (hot_possible) {
+        switch (ctx->tile_policy) {
+        case RMDA_TILE_STREAM: tile_mode = 1; break;
+        case RMDA_TILE_HOT: tile_mode = 2; break;
+        case RMDA_TILE_AUTO: tile_mode = 0; break;
+        default: {
+            const uint32_t h = __atomic_load_n(ctx->tile_hint_host, __ATOMIC_RELAXED);
+            tile_mode = h == 1u || h == 2u ? h : 0u;
+        }
+        }
+    }
     // A2 counts, offsets, block bases and the GEMM work list
     bool self_perm = false;
     if (rc == RMDA_OK) {
@@ -930,7 +975,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         // experts hold most rows (hot_min 0: never; the hot count is then 0)
         ra.n_items_hot = at<uint32_t>(ws, p.n_items_hot);
         ra.bm_hot = RMDA_GEMM_HOT_BM;
-        ra.hot_min = packed != nullptr ? ctx->hot_min : 0u;
+        ra.hot_min = hot_possible ? ctx->hot_min : 0u;
+        ra.force = tile_mode;
+        ra.hint_out = ctx->tile_policy == RMDA_TILE_ADAPTIVE && hot_possible ? ctx->tile_hint_dev : nullptr;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.sh_row0;
         // all pairs in one rank block, or few enough pairs that every block
@@ -994,7 +1041,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         }
         // the compute tile first (it has work only when the rank kernel cut
         // the list for it), then the streaming tile (work only otherwise)
-        rc = gemm_pair(ctx, s, g, gu, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), "layer gate_up");
+        rc = gemm_pair(ctx, s, g, gu, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), tile_mode, "layer gate_up");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_GATE_UP + 1);
@@ -1013,7 +1060,8 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.inter = 0;
         g.out = ye;
         g.ldo = d;
-        rc = gemm_pair(ctx, s, g, ctx->g2, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), "layer down");
+        rc = gemm_pair(ctx, s, g, ctx->g2, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), tile_mode,
+                       "layer down");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_DOWN + 1);

@@ -73,7 +73,9 @@ __device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
     return v;
 }
 
-// Top-k of one row of logits by one wave (shader/moe_route.comp:20-61):
+// Top-k of one row of logits by one wave (shader/moe_route.comp:20-61),
+// as rmda_route_row = rmda_route_load (the row into registers) then
+// rmda_route_select (the rounds):
 // topk rounds, each taking the largest untaken logit by strict '>' from
 // -3.0e38, so the lowest column wins ties and NaN / values <= -3e38 are never
 // taken; idx in selection order; z = sum_k exp(l_k - l_0) summed in
@@ -84,10 +86,8 @@ __device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
 // with device-scope loads (rows written by other workgroups of the running
 // kernel).
 template <int NV, bool AGENT>
-__device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts, uint32_t topk,
-                                               uint32_t *idx_row, float *wt_row, uint32_t *count) {
+__device__ __forceinline__ void rmda_route_load(const float *l, uint32_t experts, float (&v)[NV]) {
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
-    float v[NV];
 #pragma unroll
     for (int j = 0; j < NV; j += 1) {
         const uint32_t c = lane + RMDA_WAVE * j;
@@ -98,6 +98,15 @@ __device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts,
             v[j] = -3.0e38f;  // -3e38 is never selectable
         }
     }
+}
+
+// The selection rounds of rmda_route_row on values already in registers
+// (lane l holds columns l, l+64, ...).  sel_row, when not NULL, receives the
+// selected columns as well (e.g. an LDS copy for the caller's next step).
+template <int NV>
+__device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t topk, uint32_t *idx_row,
+                                                  float *wt_row, uint32_t *count, uint32_t *sel_row) {
+    const uint32_t lane = threadIdx.x % RMDA_WAVE;
     uint32_t taken = 0;
     // z and the per-lane output are built round by round (lane k keeps round
     // k's selection); z still accumulates in selection order
@@ -141,10 +150,21 @@ __device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts,
     if (lane < topk) {
         idx_row[lane] = my_sel;
         wt_row[lane] = expf(my_val - sv0) / z;
+        if (sel_row != nullptr) {
+            sel_row[lane] = my_sel;
+        }
         if (count != nullptr && my_sel != RMDA_NONE) {
             atomicAdd(&count[my_sel], 1u);
         }
     }
+}
+
+template <int NV, bool AGENT>
+__device__ __forceinline__ void rmda_route_row(const float *l, uint32_t experts, uint32_t topk,
+                                               uint32_t *idx_row, float *wt_row, uint32_t *count) {
+    float v[NV];
+    rmda_route_load<NV, AGENT>(l, experts, v);
+    rmda_route_select<NV>(v, topk, idx_row, wt_row, count, nullptr);
 }
 
 // Router kernel with the top-k fused in: when one workgroup's column slice
@@ -210,6 +230,9 @@ struct rmda_rank_args_t {
     uint32_t *n_items_hot;
     uint32_t bm_hot;
     uint32_t hot_min;
+    uint32_t force;       // 0: the choice above; 1: always bm items; 2: always bm_hot items
+    uint32_t *hint_out;   // or NULL: receives the choice above (1 = bm, 2 = bm_hot),
+                          // a host-visible word written with a system-scope store
     uint32_t shared_rows; // rows of the shared-expert group (0 = none)
     uint32_t shared_row0; // sorted-row base of the shared group
     // permutation written by the kernel itself when all pairs fit one rank

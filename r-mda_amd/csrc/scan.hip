@@ -19,15 +19,16 @@
 
 namespace {
 
-constexpr uint32_t NT = 256;
+constexpr uint32_t NT0 = 256;  // threads of the helper kernels and of a multi-block rank launch
 
 __global__ __launch_bounds__(256) void zero_kernel(uint32_t *p, size_t n, uint32_t value) {
-    for (size_t i = blockIdx.x * (size_t)NT + threadIdx.x; i < n; i += (size_t)gridDim.x * NT) {
+    for (size_t i = blockIdx.x * (size_t)NT0 + threadIdx.x; i < n; i += (size_t)gridDim.x * NT0) {
         p[i] = value;
     }
 }
 
-// Exclusive scan of one value per thread over a 256-thread block.
+// Exclusive scan of one value per thread over an NT-thread block.
+template <uint32_t NT>
 __device__ uint32_t block_exscan(uint32_t v, uint32_t *sbuf, uint32_t *total) {
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
     const uint32_t w = threadIdx.x / RMDA_WAVE;
@@ -101,7 +102,8 @@ __global__ __launch_bounds__(512) void scan_kernel(const uint32_t *__restrict__ 
     }
 }
 
-__global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
+template <uint32_t NT>
+__global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     __shared__ unsigned long long msk[NT / RMDA_WAVE][RMDA_MAX_EXPERTS];
     __shared__ uint32_t run[RMDA_MAX_EXPERTS];
     __shared__ uint32_t sbuf[NT / RMDA_WAVE];
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
     const uint32_t p0 = (c0 + a.tile - 1u) / a.tile * a.tile;
     const uint32_t p1 = (c1 + a.tile - 1u) / a.tile * a.tile;
     uint32_t total = 0;
-    const uint32_t base = block_exscan(p0 + p1, sbuf, &total);
+    const uint32_t base = block_exscan<NT>(p0 + p1, sbuf, &total);
     uint32_t o0 = base;
     uint32_t o1 = base + p0;
     if (a.off_in != nullptr) {
@@ -375,12 +377,16 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         const uint32_t hm = a.hot_min;
         uint32_t rows_all = 0;
         uint32_t rows_hot = 0;
-        block_exscan(c0 + c1, sbuf, &rows_all);
-        block_exscan((c0 >= hm ? c0 : 0u) + (c1 >= hm ? c1 : 0u), sbuf, &rows_hot);
+        block_exscan<NT>(c0 + c1, sbuf, &rows_all);
+        block_exscan<NT>((c0 >= hm ? c0 : 0u) + (c1 >= hm ? c1 : 0u), sbuf, &rows_hot);
         rows_all += a.shared_rows;
         rows_hot += a.shared_rows >= hm ? a.shared_rows : 0u;
-        hot = hm > 0 && rows_hot > 0 && 2ull * rows_hot >= rows_all;
+        const bool hot_auto = hm > 0 && rows_hot > 0 && 2ull * rows_hot >= rows_all;
+        hot = a.force == 2u ? true : a.force == 1u ? false : hot_auto;
         bm = hot ? a.bm_hot : a.bm;
+        if (a.hint_out != nullptr && tid == 0) {
+            __hip_atomic_store(a.hint_out, hot_auto ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         if (tid == 0) {
             *(hot ? a.n_items : a.n_items_hot) = 0u;
         }
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(256) void rank_kernel(rmda_rank_args_t a) {
         const uint32_t ni0 = (c0 + bm - 1u) / bm;
         const uint32_t ni1 = (c1 + bm - 1u) / bm;
         uint32_t n_routed = 0;
-        const uint32_t base0 = block_exscan(ni0 + ni1, sbuf, &n_routed);
+        const uint32_t base0 = block_exscan<NT>(ni0 + ni1, sbuf, &n_routed);
         uint4 *hitems = reinterpret_cast<uint4 *>(a.items);
         for (uint32_t j = 0; j < 2; j += 1) {
             const uint32_t c = j == 0 ? c0 : c1;
@@ -538,11 +544,11 @@ hipError_t rmda_launch_zero(hipStream_t s, uint32_t *p, size_t n, uint32_t value
     if (n == 0) {
         return hipSuccess;
     }
-    size_t blocks = (n + NT - 1) / NT;
+    size_t blocks = (n + NT0 - 1) / NT0;
     if (blocks > 1024) {
         blocks = 1024;
     }
-    hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)blocks), dim3(NT), 0, s, p, n, value);
+    hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)blocks), dim3(NT0), 0, s, p, n, value);
     return hipGetLastError();
 }
 
@@ -557,6 +563,6 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     if (nb == 0) {
         nb = 1;  // one block still finalises (zero counts, empty work list)
     }
-    hipLaunchKernelGGL(rank_kernel, dim3(nb), dim3(NT), 0, s, *a);
+    hipLaunchKernelGGL((rank_kernel<NT0>), dim3(nb), dim3(NT0), 0, s, *a);
     return hipGetLastError();
 }

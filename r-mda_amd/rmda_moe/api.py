@@ -105,6 +105,12 @@ class Context:
         the compute tile)."""
         self._check(self.L.rmda_moe_set_hot_rows(self.h, int(rows)))
 
+    TILE_ADAPTIVE, TILE_AUTO, TILE_STREAM, TILE_HOT = 0, 1, 2, 3
+
+    def set_tile_policy(self, policy):
+        """rmda_moe_set_tile_policy (TILE_ADAPTIVE, TILE_AUTO, TILE_STREAM, TILE_HOT)."""
+        self._check(self.L.rmda_moe_set_tile_policy(self.h, int(policy)))
+
     def _check(self, rc):
         if rc != 0:
             msg = self.L.rmda_moe_ctx_message(self.h)

@@ -21,16 +21,22 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def ctx():
+    """A context that lets the rank kernel choose the tile on every call
+    (both tiles launch), so each call's lists show its own choice."""
     torch.cuda.set_device(0)
     c = api.Context(0)
+    c.set_tile_policy(api.Context.TILE_AUTO)
     yield c
     c.set_hot_rows(256)
     c.close()
 
 
 def packed_layer(ctx, inp, packed, hot_rows):
+    """The packed layer; hot_rows None keeps the context's threshold (and its
+    adaptive tile hint: setting the threshold resets it)."""
     shape = inp["shape"]
-    ctx.set_hot_rows(hot_rows)
+    if hot_rows is not None:
+        ctx.set_hot_rows(hot_rows)
     ws = inputs.workspace_for(shape)
     ws.fill_(255)  # NaN activations wherever a task was skipped
     out = torch.full((shape["rows"], shape["d"]), float("nan"), dtype=torch.float16, device="cuda")
@@ -108,3 +114,34 @@ def test_hot_tile_against_oracle_config4(ctx):
     max_abs, rel = out_metrics(got, ref["out"])
     print("  config 4 all rows: max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_adaptive_policy_follows_previous_call():
+    """RMDA_TILE_ADAPTIVE (the default): the first call lets the rank kernel
+    choose, later calls launch only the tile the previous call chose and have
+    the rank kernel cut its list for it, even when the new call's routing
+    would choose the other tile.  Every call's output is bitwise the
+    streaming tile's."""
+    torch.cuda.set_device(0)
+    c = api.Context(0)
+    try:
+        ins = {k: inputs.make_inputs(c, configs.CONFIGS[k], seed=0) for k in (3, 4)}
+        packs = {k: pack(c, ins[k]) for k in (3, 4)}
+        # references: the streaming tile, on a context fixed to it
+        ref = {}
+        c.set_tile_policy(api.Context.TILE_STREAM)
+        for k in (3, 4):
+            ref[k], _, n_s, n_h = packed_layer(c, ins[k], packs[k], None)
+            assert n_s > 0 and n_h == 0
+        c.set_tile_policy(api.Context.TILE_ADAPTIVE)
+        # (config, tile the call must use): the first call decides on the
+        # device; each later call follows the one before it
+        seq = [(4, "hot"), (4, "hot"), (3, "hot"), (3, "stream"), (4, "stream"), (4, "hot")]
+        for k, want in seq:
+            out, _, n_s, n_h = packed_layer(c, ins[k], packs[k], None)
+            got = "hot" if n_h > 0 else "stream"
+            print("adaptive: config %d used the %s tile" % (k, got), flush=True)
+            assert got == want and (n_s == 0) == (n_h > 0)
+            assert torch.equal(out.view(torch.int16), ref[k].view(torch.int16))
+    finally:
+        c.close()
