@@ -19,6 +19,11 @@ Prints ONE JSON line.  Besides the driver's fields it carries
   decode        (config-3 runs) BASELINE configuration 2, T=128, timed the
                 same way: the weight-streaming regime's tokens/s and its two
                 GEMMs' HBM GB/s;
+  skew          (config-3 runs) BASELINE configuration 4 (Zipf-skewed load,
+                the compute tile): tokens/s and the GEMMs' TFLOP/s against
+                the dense fp16 MFMA peak;
+  fine_shared   (config-3 runs) BASELINE configuration 5 (512 experts,
+                top-10, shared expert);
   dropin        (config-3 runs) the reference-equivalent stage entry points
                 (route, scan, scatter into xp, combine) on the same inputs,
                 with their HBM GB/s.
@@ -62,6 +67,8 @@ def parse_args():
                     help="stream the HF-layout weights instead of the packed ones")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the config-2 (T=128 decode) weight-streaming line added to the config-3 run")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the config-4 (skewed, compute tile) and config-5 lines added to the config-3 run")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing the reference-equivalent stage entry points (route, scan, scatter, combine)")
     return ap.parse_args()
@@ -83,11 +90,15 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(inp, cfg, n_tokens, min_seconds=10.0, max_reps=4):
-    """Time the CPU oracle's layer on a sample of tokens (routing covers all
-    tokens, the expert FFNs only the sample), repeated until about
-    `min_seconds` of CPU work; tokens/s over the sample.  A second, much
-    smaller sample gives the single-thread figure."""
+def cpu_baseline(inp, cfg, n_tokens, rounds=7):
+    """The CPU oracle's layer (a C restatement of the reference shaders, with
+    pthreads over tokens and pairs) timed on this host: warm-up, then `rounds`
+    rounds, best and median, with the oracle's own per-stage wall clock.  A
+    round routes all T tokens (router, top-k, offsets, ranks) and runs the
+    expert FFNs and the combine for a sample of n_tokens of them, so a round
+    takes seconds; tokens/s is over the sample.  A smaller sample on one
+    thread gives the single-thread figure (the reference's bench discipline,
+    src/bench.c:32-53,93-105)."""
     import numpy as np
     from oracle import oracle as orc
     from rmda_moe import inputs
@@ -98,13 +109,17 @@ def cpu_baseline(inp, cfg, n_tokens, min_seconds=10.0, max_reps=4):
     sel = np.arange(0, T, max(1, T // n), dtype=np.uint32)[:n]
     th = cpu_threads()
     orc.lib()
-    reps, dt = 0, 0.0
-    while reps < max_reps and (reps == 0 or dt < min_seconds):
+    orc.layer(host, tile=1, rows_sel=sel[: max(1, n // 8)], threads=th)  # warm-up: pages, threads
+    times, stages = [], []
+    for _ in range(rounds):
         t0 = time.perf_counter()
-        orc.layer(host, tile=1, rows_sel=sel, threads=th)
-        dt += time.perf_counter() - t0
-        reps += 1
-    n1 = max(1, min(64, n))
+        r = orc.layer(host, tile=1, rows_sel=sel, threads=th)
+        times.append(time.perf_counter() - t0)
+        stages.append(r["stage_ms"])
+    times.sort()
+    best, med = times[0], times[len(times) // 2]
+    stage_med = {k: round(sorted(st[k] for st in stages)[len(stages) // 2], 2) for k in stages[0]}
+    n1 = max(1, min(32, n))
     sel1 = sel[:: max(1, len(sel) // n1)][:n1]
     t0 = time.perf_counter()
     orc.layer(host, tile=1, rows_sel=sel1, threads=1)
@@ -117,16 +132,26 @@ def cpu_baseline(inp, cfg, n_tokens, min_seconds=10.0, max_reps=4):
                 break
     except OSError:
         pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
     return {
-        "value": round(reps * len(sel) / dt, 2),
+        "value": round(len(sel) / med, 2),
         "unit": "tokens/s",
         "cores": th,
         "kind": "port",
-        "sample": "%d of %d tokens (every %d-th) through the CPU oracle's full layer "
-                  "(router+top-k for all %d tokens, expert FFNs for the sample) x %d passes, %d threads, "
-                  "%.1f s, %s" % (len(sel), T, max(1, T // n), T, reps, th, dt, model),
+        "best_tokens/s": round(len(sel) / best, 2),
+        "rounds": rounds,
+        "best_s": round(best, 3),
+        "median_s": round(med, 3),
+        "stage_ms_median": stage_med,
+        "host": {"cpu": model, "nproc": os.cpu_count(), "affinity": affinity, "threads_used": th},
+        "sample": "per round: routing of all %d tokens, expert FFNs + combine for %d of them (every %d-th); "
+                  "%d threads (the box's CPU share for one GPU is 16); median of %d rounds after a warm-up"
+                  % (T, len(sel), max(1, T // n), th, rounds),
         "single_thread": {"value": round(len(sel1) / dt1, 2), "unit": "tokens/s",
-                          "sample": "%d tokens, 1 thread, %.1f s" % (len(sel1), dt1)},
+                          "sample": "routing of all %d tokens + FFNs of %d, 1 thread, %.1f s" % (T, len(sel1), dt1)},
     }
 
 
@@ -168,12 +193,15 @@ def measure_peaks(torch):
             "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
 
 
-def measure_decode(ctx, torch, steps=100, warmup=50):
-    """BASELINE config 2 (T=128 decode), the weight-streaming regime: the
-    layer's rate and its two GEMMs' HBM rates, timed as the main line."""
+def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
+    """Another BASELINE configuration on the same context, timed as the main
+    line: the layer's rate, and each grouped GEMM's time, TFLOP/s and HBM
+    GB/s against the published peaks (algorithmic work; experts touched
+    counted from the run's routing).  Config 2 is the weight-streaming
+    regime (HBM-bound), config 4 the compute-bound one (hot experts)."""
     from rmda_moe import api, configs, inputs
 
-    cfg = configs.CONFIGS[2]
+    cfg = configs.CONFIGS[cfg_id]
     inp = inputs.make_inputs(ctx, cfg, seed=0)
     shape = inp["shape"]
     ws = inputs.workspace_for(shape)
@@ -200,16 +228,26 @@ def measure_decode(ctx, torch, steps=100, warmup=50):
     for _ in range(steps):
         step()
     stage_ms, n_prof = ctx.prof_end()
-    counts = api.ws_views(shape, ws)["count"].cpu().numpy()
-    work = configs.algorithmic_work(cfg, touched=int((counts > 0).sum()))
-    res = {"workload": "decode: T=%d d=%d experts=%d top-%d inter=%d (BASELINE config 2)"
-                       % (shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"]),
-           "tokens/s": round(shape["rows"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 5), "steps": steps}
     event_us = 1000.0 * ctx.prof_empty_ms() / max(n_prof, 1)
+    views = api.ws_views(shape, ws)
+    counts = views["count"].cpu().numpy()
+    hot = int(views["n_items_hot"].cpu().numpy()[0]) > 0
+    work = configs.algorithmic_work(cfg, touched=int((counts > 0).sum()))
+    res = {"workload": "%s: T=%d d=%d experts=%d top-%d inter=%d shared=%d%s (BASELINE config %d)"
+                       % (cfg["name"], shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"],
+                          shape["shared"], " skewed" if cfg.get("skew") else "", cfg_id),
+           "tokens/s": round(shape["rows"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 5), "steps": steps,
+           "experts_touched": int((counts > 0).sum()), "gemm_tile": "compute (hot experts)" if hot else "streaming"}
+    gemm_us = 0.0
     for k in ("gate_up", "down"):
         us = 1000.0 * stage_ms[k] / max(n_prof, 1) - event_us
+        gemm_us += us
         gbs = work[k + "_bytes"] / (us * 1e-6) / 1e9
-        res[k] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        tf = work[k + "_flops"] / (us * 1e-6) / 1e12
+        res[k] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16_TFLOPS, 4),
+                  "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    tf = work["gemm_flops"] / (gemm_us * 1e-6) / 1e12
+    res["gemm"] = {"TFLOP/s": round(tf, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
     del inp, ws, out, packed
     torch.cuda.empty_cache()
     return res
@@ -431,6 +469,20 @@ def main():
     event_us = 1000.0 * ctx.prof_empty_ms() / max(n_prof, 1)
     stage_us = {k: 1000.0 * v / max(n_prof, 1) - event_us for k, v in stage_ms.items() if v > 0}
 
+    # steady state, reported beside (never in place of) the timed region:
+    # the GPU's clocks take tens of milliseconds of back-to-back calls to
+    # settle, so a short --warmup times part of that transient
+    for _ in range(100):
+        step()
+    e_s0 = torch.cuda.Event(enable_timing=True)
+    e_s1 = torch.cuda.Event(enable_timing=True)
+    e_s0.record()
+    for _ in range(100):
+        step()
+    e_s1.record()
+    torch.cuda.synchronize()
+    steady_ms = e_s0.elapsed_time(e_s1) / 100
+
     views = api.ws_views(shape, ws)
     counts = views["count"].cpu().numpy()
     touched = int((counts > 0).sum())
@@ -492,14 +544,18 @@ def main():
 
     peaks = None if args.no_peaks else measure_peaks(torch)
     upload = measure_upload(ctx, shape, torch) if args.upload else None
-    decode = measure_decode(ctx, torch) if (args.config == 3 and not args.no_decode) else None
+    decode = measure_config(ctx, torch, 2) if (args.config == 3 and not args.no_decode) else None
+    others = {}
+    if args.config == 3 and not args.no_others:
+        others["skew"] = measure_config(ctx, torch, 4)
+        others["fine_shared"] = measure_config(ctx, torch, 5)
     dropin = measure_dropins(ctx, torch, inp) if (args.config == 3 and not args.no_dropin) else None
 
     cpu = None
     if not args.no_cpu_baseline:
         n_tok = args.cpu_tokens
         if n_tok is None:
-            n_tok = {1: 256, 2: 128, 3: 2048, 4: 2048, 5: 1024}[args.config]
+            n_tok = {1: 256, 2: 128, 3: 512, 4: 512, 5: 256}[args.config]
         cpu = cpu_baseline(inp, cfg, n_tok)
 
     if args.stages:
@@ -529,12 +585,16 @@ def main():
         "rounds": {"n": n_rounds, "best_ms": round(round_ms[0], 5),
                    "median_ms": round(round_ms[len(round_ms) // 2], 5),
                    "ms_in_order": [round(x, 4) for x in round_seq]},
+        "steady_state": {"ms_per_step": round(steady_ms, 5), "tokens/s": round(T / (steady_ms * 1e-3), 1),
+                         "what": "100 calls timed after the timed region, the stage profile and 100 more calls"},
         "weights": "HF layout" if args.hf_layout else "packed once before timing (%.1f ms, host-timed)" % pack_ms,
         "roofline": roof,
         "gemm": gemm,
         "hbm": hbm_small,
         "stages": stages,
         "decode": decode,
+        "skew": others.get("skew"),
+        "fine_shared": others.get("fine_shared"),
         "dropin": dropin,
         "cpu_baseline": cpu,
     }

@@ -19,6 +19,7 @@
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ------------------------------------------------------------------ */
 /* fp16 conversion                                                     */
@@ -693,6 +694,12 @@ static float orc_scaled_cast(const float *src, uint16_t *dst, size_t n, int scal
     return 1.0f / orc_slot_scale(&amax, pc.slot);
 }
 
+static double orc_now_ms(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec * 1e-6;
+}
+
 int orc_moe_layer(const orc_layer_t *L) {
     const rmda_moe_shape_t *S = &L->shape;
     uint32_t T = S->rows;
@@ -713,16 +720,28 @@ int orc_moe_layer(const orc_layer_t *L) {
     uint32_t *off = L->off ? L->off : malloc(sizeof(uint32_t) * E);
     uint32_t *fill = calloc(E, sizeof(uint32_t));
 
+    double t_mark = orc_now_ms();
+    double st[ORC_LAYER_STAGES] = {0};
+#define ORC_STAGE(i)                   \
+    do {                               \
+        const double t_now = orc_now_ms(); \
+        st[i] += t_now - t_mark;       \
+        t_mark = t_now;                \
+    } while (0)
     /* A0: router projection (x . [W_router; w_shared_gate]^T), canonical order */
     rmda_moe_router_t pr = {.rows = T, .d = d, .cols = ps, .stride = ps, .nbias = E};
     orc_router(&pr, L->x, L->w_router, L->bias, proj, th);
+    ORC_STAGE(0);
     /* A1-A3: route, scan, scatter (slots only; the GEMMs read token rows) */
     rmda_pc_moe_route_t pc_r = {.rows = T, .experts = E, .topk = K, .stride = ps};
     orc_moe_route(&pc_r, proj, idx, wt, count);
+    ORC_STAGE(1);
     rmda_pc_moe_scan_t pc_s = {.experts = E, .tile = L->tile};
     orc_moe_scan(&pc_s, count, off, NULL, 0);
+    ORC_STAGE(2);
     rmda_pc_moe_scatter_t pc_t = {.rows = T, .topk = K, .d8 = d / 8};
     orc_moe_scatter(&pc_t, idx, off, fill, NULL, NULL, slot);
+    ORC_STAGE(3);
 
     /* activations fed to the GEMMs: x, optionally power-of-two scaled
      * (src/qwen.c:844; bit-neutral for in-range values) */
@@ -763,9 +782,16 @@ int orc_moe_layer(const orc_layer_t *L) {
     job.hp16 = malloc(sizeof(uint16_t) * (size_t)n_pairs * I + 2);
     orc_parallel(n_pairs, orc_ffn_up_item, &job, th);
     job.shp = orc_scaled_cast(job.hp, job.hp16, (size_t)n_pairs * I, L->hp_scale);
+    ORC_STAGE(4);
     /* A7: down (src/qwen.c:878) */
     job.ye = malloc(sizeof(float) * (size_t)n_pairs * d + 4);
     orc_parallel(n_pairs, orc_ffn_down_item, &job, th);
+    if (L->ye16) {
+        for (size_t i = 0; i < (size_t)n_pairs * d; i += 1) {
+            job.ye[i] = orc_h2f(orc_f2h(job.ye[i]));
+        }
+    }
+    ORC_STAGE(5);
     /* A8: shared expert (src/qwen.c:879-886) */
     if (S->shared > 0) {
         uint32_t Is = S->shared;
@@ -775,7 +801,13 @@ int orc_moe_layer(const orc_layer_t *L) {
         job.shs = orc_scaled_cast(job.hs, job.hs16, (size_t)n_tok * Is, L->hp_scale);
         job.sh = malloc(sizeof(float) * (size_t)n_tok * d + 4);
         orc_parallel(n_tok, orc_shared_down_item, &job, th);
+        if (L->ye16) {
+            for (size_t i = 0; i < (size_t)n_tok * d; i += 1) {
+                job.sh[i] = orc_h2f(orc_f2h(job.sh[i]));
+            }
+        }
     }
+    ORC_STAGE(6);
     /* A9: combine, plain mode, in j order (moe_combine.comp:31-35); ye rows
      * are per selected pair, so slot here is the pair's position. */
     for (uint32_t t = 0; t < n_tok; t += 1) {
@@ -792,6 +824,11 @@ int orc_moe_layer(const orc_layer_t *L) {
             }
             L->out[(size_t)t * d + c] = acc;
         }
+    }
+    ORC_STAGE(7);
+#undef ORC_STAGE
+    if (L->stage_ms != NULL) {
+        memcpy(L->stage_ms, st, sizeof(st));
     }
     free(job.hp);
     free(job.hp16);

@@ -107,7 +107,15 @@ typedef struct orc_layer_t {
     uint32_t *slot;
     uint32_t *count;
     uint32_t *off;
+    /* nonzero: round every expert output row (ye) to fp16 before the
+     * combine, as the fused GPU layer stores it (the reference keeps fp32) */
+    int ye16;
+    /* or NULL: wall-clock ms of the layer's stages, in the order
+     * router, route, scan, scatter, gate_up (+SwiGLU, cast), down, shared
+     * expert, combine (ORC_LAYER_STAGES) */
+    double *stage_ms;
 } orc_layer_t;
+#define ORC_LAYER_STAGES 8
 
 int orc_moe_layer(const orc_layer_t *L);
 uint32_t orc_proj_stride(const rmda_moe_shape_t *s);

@@ -71,7 +71,9 @@ class Layer(ctypes.Structure):
                 ("x", _p), ("w_router", _p), ("bias", _p), ("w_gate_up", _p), ("w_down", _p),
                 ("w_sh_gate_up", _p), ("w_sh_down", _p), ("rows_sel", _p), ("n_sel", _u32),
                 ("out", _p), ("proj", _p), ("idx", _p), ("wt", _p), ("slot", _p), ("count", _p),
-                ("off", _p)]
+                ("off", _p), ("ye16", ctypes.c_int), ("stage_ms", _p)]
+
+LAYER_STAGES = ("router", "route", "scan", "scatter", "gate_up", "down", "shared", "combine")
 
 
 def build():
@@ -283,12 +285,14 @@ def proj_stride(experts, shared):
     return experts + (1 if shared > 0 else 0)
 
 
-def layer(inp, tile=1, hp_scale=1, x_scale=1, rows_sel=None, threads=None):
+def layer(inp, tile=1, hp_scale=1, x_scale=1, rows_sel=None, threads=None, ye16=False):
     """Whole layer in the reference order (plain output, fp32).
 
     `inp` is a dict of host numpy arrays (see rmda_moe.inputs): x, w_router,
     bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down and the shape fields.
-    Returns a dict with out and the routing intermediates.
+    ye16 rounds every expert output row to fp16 before the combine (the
+    fused GPU layer's storage).  Returns a dict with out, the routing
+    intermediates and stage_ms (wall-clock ms per stage, LAYER_STAGES).
     """
     s = inp["shape"]
     T, d, E, K = s["rows"], s["d"], s["experts"], s["topk"]
@@ -324,7 +328,11 @@ def layer(inp, tile=1, hp_scale=1, x_scale=1, rows_sel=None, threads=None):
     L.n_sel = 0 if sel is None else sel.shape[0]
     for k in ["out", "proj", "idx", "wt", "slot", "count", "off"]:
         setattr(L, k, _ptr(res[k]))
+    L.ye16 = 1 if ye16 else 0
+    stage_ms = np.zeros(len(LAYER_STAGES), np.float64)
+    L.stage_ms = _ptr(stage_ms)
     rc = lib().orc_moe_layer(_ref(L))
+    res["stage_ms"] = dict(zip(LAYER_STAGES, stage_ms.tolist()))
     if rc != 0:
         raise ValueError("oracle layer rejected the shape %r" % (s,))
     return res
