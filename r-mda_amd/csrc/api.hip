@@ -689,6 +689,9 @@ int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t 
     g.amax = amax;
     g.sa = pc->sa;
     g.sb = pc->sb;
+    if (rmda_ref_mm_supported(&g)) {
+        return hip_check(ctx, rmda_launch_ref_mm(ctx->stream, &g, ctx->g2.grid), "moe_mm");
+    }
     return hip_check(ctx, rmda_launch_gemm(ctx->stream, &g), "moe_mm");
 }
 

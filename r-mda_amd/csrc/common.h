@@ -298,6 +298,11 @@ struct rmda_gemm_args_t {
     uint32_t sa, sb;
 };
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
+// gemm_ref.hip: the F32 (reference matmul_f16_moe) contract on the
+// persistent LDS-DMA pipeline, for n % 256 == 0, k % 64 == 0 and at most
+// 4096 row tiles; rmda_launch_gemm covers the rest.
+bool rmda_ref_mm_supported(const rmda_gemm_args_t *a);
+hipError_t rmda_launch_ref_mm(hipStream_t s, const rmda_gemm_args_t *a, uint32_t grid);
 #define RMDA_GEMM_BM 128u
 
 // gemm2.hip: the fused layer's grouped GEMM (SWIGLU and F16 modes) over

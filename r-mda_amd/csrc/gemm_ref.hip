@@ -1,0 +1,267 @@
+// The reference's grouped GEMM contract (matmul_f16_moe, rmda_moe_mm) on the
+// LDS-DMA pipeline: C[m][n] = A[m]·B[tiles[m/128]][n]ᵀ / (scale(sa)·scale(sb))
+// for every 128-row tile t of A whose tiles[t] names an expert
+// (shader/matmul_f16_moe.comp:70-126, src/qwen.c:770-786).  A is the
+// permuted activation copy xp [m][k] and B the HF-layout expert weights
+// [E][n][k], both fp16 row-major, C fp32.
+//
+//   * Persistent: one 768-thread workgroup per CU walks tasks (valid tile,
+//     256-column N tile).  Each workgroup first compacts the valid tiles of
+//     tiles[] into LDS, so tiles marked RMDA_NONE cost nothing and any order
+//     of tiles[] is accepted; tasks are dealt to the XCDs in contiguous runs
+//     (chunk_sched_t), so the N tiles of a row tile and the tiles of one
+//     expert meet in one L2 and its weight lines are fetched from HBM once.
+//   * K step 64: every A row and every weight row of a stage is one whole
+//     128-byte line (the HF layout read 32 halves at a time would split each
+//     line over two stages).  A (128 x 64) and B (256 x 64) go straight into
+//     LDS with global_load_lds_dwordx4 through a 3-stage ring of 48 KiB; a
+//     row's 16-byte chunk c sits at slot c ^ ((r >> 1) & 7), which keeps the
+//     16-lane fragment reads free of bank conflicts.
+//   * 8 MFMA waves = 2 (M, 64 rows) x 4 (N, 64 columns),
+//     v_mfma_f32_16x16x32_f16, fp32 accumulate; they also write C.  Four more
+//     waves issue all of the DMA (4 A and 8 B instructions per stage each) and
+//     nothing else.  On gfx950 a wave's stores count in vmcnt like its loads,
+//     so a wave that both streamed the stages and wrote a finished tile's
+//     128 KiB of fp32 C would drain its whole load pipeline at every wait
+//     after a tile; measured at BASELINE config 3, the stores then cost
+//     gate_up 122 of 327 us.  With the split the issue waves' waits count
+//     their own loads only (gate_up 327 -> 260 us), and C goes out with
+//     non-temporal stores, written once and not read again here
+//     (260 -> 247 us).
+#include "common.h"
+#include "gemm_sched.h"
+
+namespace {
+
+using namespace rmda_gemm;
+
+constexpr uint32_t RM = 128;   // rows per tile (the reference's P)
+constexpr uint32_t RN = 256;   // N tile
+constexpr uint32_t RK = 64;    // K step
+constexpr uint32_t RMW = 8;    // MFMA waves: 2 (M, 64 rows) x 4 (N, 64 columns)
+constexpr uint32_t RIW = 4;    // DMA issue waves
+constexpr uint32_t RSTAGES = 3;
+constexpr uint32_t MAX_TILES = 4096;  // compacted tile list in LDS (u16 entries)
+
+__device__ __forceinline__ float ref_slot_scale(const uint32_t *amax, uint32_t slot) {
+    if (slot == RMDA_NO_SLOT || amax == nullptr) {
+        return 1.0f;
+    }
+    const uint32_t u = amax[slot];
+    const float a = __builtin_bit_cast(float, u);
+    if (!(a > 0.0f) || __builtin_isinf(a)) {
+        return 1.0f;
+    }
+    return ldexpf(1.0f, 141 - (int)((u >> 23) & 0xffu));
+}
+
+__global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
+    constexpr uint32_t CH = RK / 8;                 // 16-byte chunks per row
+    constexpr uint32_t RPI = 64 / CH;               // rows per DMA instruction
+    constexpr uint32_t A_BYTES = RM * RK * 2;       // 16 KiB
+    constexpr uint32_t B_BYTES = RN * RK * 2;       // 32 KiB
+    constexpr uint32_t STAGE_BYTES = A_BYTES + B_BYTES;
+    constexpr uint32_t A_PER = RM / RPI / RIW;      // 4 A instructions per issue wave per stage
+    constexpr uint32_t B_PER = RN / RPI / RIW;      // 8 B instructions
+    constexpr uint32_t L_PER = A_PER + B_PER;
+    static_assert(A_PER * RPI * RIW == RM && B_PER * RPI * RIW == RN, "DMA split");
+    static_assert(2 * L_PER < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[RSTAGES * STAGE_BYTES];
+    __shared__ uint16_t tl[MAX_TILES];
+    __shared__ uint32_t nv_w[RMW + RIW];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % RMDA_WAVE;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
+
+    // ---- compact the valid tiles (tiles[t] != NONE) into tl[], in order ----
+    constexpr uint32_t NTH = (RMW + RIW) * RMDA_WAVE;
+    const uint32_t n_all = g.max_items;
+    uint32_t n_valid = 0;
+    for (uint32_t base = 0; base < n_all; base += NTH) {
+        const uint32_t t = base + tid;
+        const bool ok = t < n_all && g.tiles[t] != RMDA_NONE;
+        const uint64_t m = __ballot(ok);
+        if (lane == 0) {
+            nv_w[w] = (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        uint32_t before = n_valid;
+        uint32_t all = 0;
+        for (uint32_t q = 0; q < RMW + RIW; q += 1) {
+            before += q < w ? nv_w[q] : 0u;
+            all += nv_w[q];
+        }
+        if (ok) {
+            const uint64_t below = lane == 0 ? 0ull : (~0ull >> (RMDA_WAVE - lane));
+            tl[before + (uint32_t)__popcll(m & below)] = (uint16_t)t;
+        }
+        n_valid += all;
+        __syncthreads();
+    }
+    const uint32_t ntiles = g.n_w / RN;
+    const chunk_sched_t sched(n_valid, ntiles);
+    const uint32_t ntask = sched.ntask;
+    if (ntask == 0) {
+        return;
+    }
+    const uint32_t steps = g.k / RK;
+    const uint32_t nstage = ntask * steps;
+
+    if (w >= RMW) {
+        // ================= issue waves: DMA only, so their vmcnt counts loads only =================
+        const uint32_t dw = w - RMW;
+        const uint32_t lrow = lane / CH;
+        const uint32_t lch = lane % CH;
+        const uint16_t *a_src[A_PER];
+        const uint16_t *b_src[B_PER];
+        auto setup = [&](uint32_t q) __attribute__((always_inline)) {
+            uint32_t nt;
+            const uint32_t t = tl[sched.item(q, nt)];
+            const uint32_t grp = g.tiles[t];
+            const uint16_t *wg = g.w + (size_t)grp * g.n_w * g.k;
+#pragma unroll
+            for (uint32_t j = 0; j < A_PER; j += 1) {
+                const uint32_t r = (dw * A_PER + j) * RPI + lrow;
+                a_src[j] = g.a + (size_t)(t * RM + r) * g.lda + (lch ^ swz<RK>(r)) * 8;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                const uint32_t n = (dw * B_PER + j) * RPI + lrow;
+                b_src[j] = wg + (size_t)(nt * RN + n) * g.k + (lch ^ swz<RK>(n)) * 8;
+            }
+        };
+        uint32_t i_task = 0;
+        uint32_t i_s = 0;
+        setup(0);
+        auto issue = [&](uint32_t buf) __attribute__((always_inline)) {
+            if (i_s == steps) {
+                i_task += 1;
+                i_s = 0;
+                setup(i_task);
+            }
+            uint8_t *base = smem + buf * STAGE_BYTES;
+#pragma unroll
+            for (uint32_t j = 0; j < A_PER; j += 1) {
+                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + i_s * RK),
+                                                 (lds_void_t *)(base + (dw * A_PER + j) * RPI * (RK * 2)), 16, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < B_PER; j += 1) {
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)(b_src[j] + i_s * RK),
+                    (lds_void_t *)(base + A_BYTES + (dw * B_PER + j) * RPI * (RK * 2)), 16, 0, 0);
+            }
+            i_s += 1;
+        };
+        // two barriers per stage: the second one, after the MFMA waves have
+        // read the stage into registers, frees its buffer, so all RSTAGES
+        // buffers are in flight
+#pragma unroll
+        for (uint32_t st = 0; st < RSTAGES; st += 1) {
+            if (st < nstage) {
+                issue(st);
+            }
+        }
+        uint32_t ibuf = 0;
+        for (uint32_t gs = 0; gs < nstage; gs += 1) {
+            wait_after<L_PER>(min(nstage - 1 - gs, RSTAGES - 1));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_s_barrier();
+            if (gs + RSTAGES < nstage) {
+                issue(ibuf);
+                ibuf = ibuf + 1 == RSTAGES ? 0 : ibuf + 1;
+            }
+        }
+        return;
+    }
+
+    // ================= MFMA waves: fragments, MFMAs and the fp32 stores =================
+    const uint32_t wm = w / 4;
+    const uint32_t wn = w % 4;
+    const uint32_t fr = lane % 16;
+    const uint32_t fq = lane / 16;
+    const uint32_t a_row = (wm * 64 + fr) * (RK * 2);
+    const uint32_t b_row = A_BYTES + (wn * 64 + fr) * (RK * 2);
+    const uint32_t c0 = ((0u + fq) ^ swz<RK>(fr)) * 16;  // chunk of K half 0
+    const uint32_t c1 = ((4u + fq) ^ swz<RK>(fr)) * 16;  // chunk of K half 1
+    const uint32_t rq = 4 * fq;
+    const float sc = 1.0f / (ref_slot_scale(g.amax, g.sa) * ref_slot_scale(g.amax, g.sb));
+    float *C = reinterpret_cast<float *>(g.out);
+    floatx4_t acc[4][4];
+    uint32_t kc = 0;
+    uint32_t ks = 0;
+    uint32_t cbuf = 0;
+    for (uint32_t gs = 0; gs < nstage; gs += 1) {
+        lds_barrier();
+        const uint8_t *base = smem + cbuf * STAGE_BYTES;
+        cbuf = cbuf + 1 == RSTAGES ? 0 : cbuf + 1;
+        half8_t fa[2][4], fb[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; i += 1) {
+            fa[0][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c0);
+            fb[0][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c0);
+            fa[1][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c1);
+            fb[1][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c1);
+        }
+        lds_barrier();  // the stage is in registers: the issue waves may refill its buffer
+        if (ks == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t kk = 0; kk < 2; kk += 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int j = 0; j < 4; j += 1) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (ks == steps - 1) {
+            // acc[i][j][v] = C[tile row wm*64 + i*16 + 4*(lane/16) + v][wn*64 + j*16 + lane%16]
+            uint32_t nt;
+            const uint32_t t = tl[sched.item(kc, nt)];
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+#pragma unroll
+                for (int v = 0; v < 4; v += 1) {
+                    const size_t r = (size_t)t * RM + wm * 64 + i * 16 + rq + v;
+#pragma unroll
+                    for (int j = 0; j < 4; j += 1) {
+                        __builtin_nontemporal_store(acc[i][j][v] * sc, &C[r * g.ldo + nt * RN + wn * 64 + j * 16 + fr]);
+                    }
+                }
+            }
+        }
+        ks += 1;
+        if (ks == steps) {
+            ks = 0;
+            kc += 1;
+        }
+    }
+}
+
+}  // namespace
+
+bool rmda_ref_mm_supported(const rmda_gemm_args_t *a) {
+    return a->n_w % RN == 0 && a->k % RK == 0 && a->max_items <= MAX_TILES;
+}
+
+hipError_t rmda_launch_ref_mm(hipStream_t s, const rmda_gemm_args_t *a, uint32_t grid) {
+    if (!rmda_ref_mm_supported(a)) {
+        return hipErrorInvalidValue;
+    }
+    if (a->max_items == 0) {
+        return hipSuccess;
+    }
+    const dim3 gr(grid >= 8 ? grid / 8 * 8 : 8);
+    hipLaunchKernelGGL(ref_mm_kernel, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+    return hipGetLastError();
+}

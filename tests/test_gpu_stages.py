@@ -286,6 +286,10 @@ def test_scatter_twice_deterministic(ctx):
 # ---------------------------------------------------------------- grouped GEMM (A4/A7, drop-in)
 
 @pytest.mark.parametrize("m,n,k,E,scaled", [(512, 256, 512, 3, False), (640, 1536, 2048, 5, True),
+                                           # 600 row tiles: the valid-tile list is compacted in two passes
+                                           (76800, 256, 64, 7, False),
+                                           (4096, 512, 768, 9, True),
+                                           # n % 256 != 0, k % 64 != 0: the register-staged kernel
                                            (256, 128, 32, 2, False)])
 def test_moe_mm_vs_oracle(ctx, m, n, k, E, scaled):
     r = rng(m + n + k)
