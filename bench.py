@@ -71,6 +71,9 @@ def parse_args():
                     help="skip the config-4 (skewed, compute tile) and config-5 lines added to the config-3 run")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing the reference-equivalent stage entry points (route, scan, scatter, combine)")
+    ap.add_argument("--transient", action="store_true",
+                    help="before the warm-up, time each of the first 400 layer calls of this fresh process, "
+                         "then 60 more after a 2 s idle (the GPU's warm-up transient)")
     return ap.parse_args()
 
 
@@ -191,6 +194,33 @@ def measure_peaks(torch):
     torch.cuda.empty_cache()
     return {"hbm_copy_GB/s": round(copy_gbs, 1), "hbm_copy": "1 GiB device copy, 2*bytes/t",
             "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
+
+
+def measure_transient(step, torch, n=400, n_after=60, idle_s=2.0):
+    """Per-call GPU time of the first n layer calls of a fresh process, one
+    event between consecutive calls, then n_after calls after idle_s of
+    idling.  Shows how long the GPU takes to reach its steady rate, and
+    whether the slow calls return after an idle gap with every buffer already
+    touched (which rules out first-touch and TLB costs)."""
+    def run(k):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(k + 1)]
+        torch.cuda.synchronize()
+        evs[0].record()
+        for i in range(k):
+            step()
+            evs[i + 1].record()
+        torch.cuda.synchronize()
+        return [evs[i].elapsed_time(evs[i + 1]) for i in range(k)]
+
+    first = run(n)
+    time.sleep(idle_s)
+    after = run(n_after)
+    blocks = [first[a:a + 20] for a in range(0, n, 20)]
+    return {"what": "per-call ms of the first %d calls of the process (before any warm-up), in blocks of 20, "
+                    "then %d calls after %.0f s idle" % (n, n_after, idle_s),
+            "block_mean_ms": [round(sum(b) / len(b), 4) for b in blocks],
+            "block_min_ms": [round(min(b), 4) for b in blocks],
+            "after_idle_ms": [round(x, 4) for x in after]}
 
 
 def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
@@ -434,6 +464,7 @@ def main():
             ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws,
                       packed=packed)
 
+    transient = measure_transient(step, torch) if args.transient else None
     for _ in range(args.warmup):
         step()
     ctx.sync()
@@ -602,10 +633,21 @@ def main():
         line["cpu_baseline"]["gpu_over_cpu"] = round(line["value"] / cpu["value"], 1)
     if upload is not None:
         line["upload"] = upload
+    if transient is not None:
+        line["transient"] = transient
     if peaks is not None:
         line["peaks_measured"] = peaks
         if roof["unit"] == "GB/s":
             roof["frac_of_measured_copy"] = round(roof["achieved"] / peaks["hbm_copy_GB/s"], 4)
+        # the copy-shaped stages beside this box's own device-copy rate: a
+        # scatter or combine cannot stream faster than a plain copy does
+        cp = peaks["hbm_copy_GB/s"]
+        if hbm_small.get("combine_GB/s"):
+            hbm_small["combine_frac_of_measured_copy"] = round(hbm_small["combine_GB/s"] / cp, 4)
+        if dropin is not None:
+            for k in ("scatter", "combine_hc", "combine_plain"):
+                if "GB/s" in dropin.get(k, {}):
+                    dropin[k]["frac_of_measured_copy"] = round(dropin[k]["GB/s"] / cp, 4)
     ctx.close()
     print(json.dumps(line), flush=True)
 
