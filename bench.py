@@ -560,7 +560,7 @@ def main():
     gemm = {"TFLOP/s": round(gemm_tf, 1), "frac_of_fp16_peak": round(gemm_tf / PEAK_FP16_TFLOPS, 4),
             "ai_flop_per_byte": round(ai, 1), "ceiling_TFLOP/s": round(ceiling, 1),
             "frac_of_ceiling": round(gemm_tf / ceiling, 4), "experts_touched": touched}
-    hbm_small = {"combine_GB/s": stages["combine"].get("GB/s")}
+    hbm_small = {"combine_GB/s": stages.get("combine", {}).get("GB/s")}
     stages["event_interval_us"] = round(event_us, 2)
 
     if args.calib_copy:

@@ -168,6 +168,16 @@ int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows);
  * only. */
 enum { RMDA_TILE_ADAPTIVE = 0, RMDA_TILE_AUTO = 1, RMDA_TILE_STREAM = 2, RMDA_TILE_HOT = 3 };
 int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy);
+/* Fold the combine into the down GEMM (replaces moe_combine's own dispatch,
+ * src/qwen.c:887-906, inside rmda_moe_layer; off by default).  Each down-GEMM
+ * wave that stores the last of a token's rows for 64 output columns sums
+ * them there, in j order, exactly as the combine kernel does, so the output
+ * is bitwise the same; the fused layer then launches no combine kernel when
+ * the streaming tile runs.  Packed weights only (otherwise ignored).
+ * Slower on MI355X (layer 0.296 -> 0.346 ms): the rows
+ * must be stored through to the device coherence point and counted with
+ * device-scope atomics, because a token's rows are stored on several XCDs. */
+int rmda_moe_set_fused_combine(rmda_moe_ctx_t *ctx, int on);
 /* Sticky error: RMDA_OK or the first failure's code, with a message. */
 int rmda_moe_ctx_error(const rmda_moe_ctx_t *ctx);
 const char *rmda_moe_ctx_message(const rmda_moe_ctx_t *ctx);

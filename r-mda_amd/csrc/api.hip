@@ -42,6 +42,9 @@ struct rmda_moe_ctx {
     int tile_policy;
     uint32_t *tile_hint_host;
     uint32_t *tile_hint_dev;
+    // combine folded into the down GEMM (rmda_moe_set_fused_combine;
+    // RMDA_MOE_FUSED_COMBINE sets the initial value)
+    int fused_combine;
     // stage profiler: a ring of per-call event sets, harvested when full
     int prof_on;
     int prof_made;
@@ -134,8 +137,17 @@ int prof_harvest(rmda_moe_ctx_t *c) {
     if (c->prof_pending == 0) {
         return RMDA_OK;
     }
-    int rc = hip_check(c, hipEventSynchronize(c->prof_ev[c->prof_pending - 1][RMDA_PROF_STAGES]),
-                       "profiler hipEventSynchronize");
+    // the last event the last pending call recorded (a skipped final stage,
+    // e.g. a combine folded into the down GEMM, records none)
+    const uint32_t lp = c->prof_pending - 1;
+    uint32_t ev_last = RMDA_PROF_STAGES + 1;
+    for (uint32_t st = RMDA_PROF_STAGES; st-- > 0;) {
+        if (((c->prof_skip[lp] >> st) & 1u) == 0) {
+            ev_last = st + 1;
+            break;
+        }
+    }
+    int rc = hip_check(c, hipEventSynchronize(c->prof_ev[lp][ev_last]), "profiler hipEventSynchronize");
     for (uint32_t i = 0; i < c->prof_pending && rc == RMDA_OK; i += 1) {
         float ms = 0.0f;
         rc = hip_check(c, hipEventElapsedTime(&ms, c->prof_ev[i][0], c->prof_ev[i][RMDA_PROF_STAGES + 1]),
@@ -181,7 +193,8 @@ void prof_skip(rmda_moe_ctx_t *c, uint32_t st) {
 }
 
 struct LayerPlan {
-    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, ye, total;
+    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, ye, fc_cnt,
+        total;
     uint32_t ps, npairs, nblocks, max_items, sh_rows, sh_row0, groups_rows;
 };
 
@@ -251,6 +264,8 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     p.items = take((size_t)p.max_items * 16);
     p.hp = take((size_t)p.groups_rows * s->inter * 2);
     p.ye = take((size_t)p.groups_rows * s->d * 2);
+    // arrival counters of the folded combine, one per (token, 64 columns)
+    p.fc_cnt = take((size_t)T * (s->d / RMDA_FC_COLS) * 4);
     p.total = o;
     return p;
 }
@@ -360,6 +375,10 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
     c->hot_sched = 0;
     if (const char *v = getenv("RMDA_MOE_HOT_SCHED")) {
         c->hot_sched = atoi(v);
+    }
+    c->fused_combine = 0;
+    if (const char *v = getenv("RMDA_MOE_FUSED_COMBINE")) {
+        c->fused_combine = atoi(v) != 0 ? 1 : 0;
     }
     c->tile_policy = RMDA_TILE_ADAPTIVE;
     if (const char *v = getenv("RMDA_MOE_TILE_POLICY")) {  // tuning only
@@ -493,6 +512,14 @@ int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy) {
     }
     ctx->tile_policy = policy;
     __atomic_store_n(ctx->tile_hint_host, 0u, __ATOMIC_RELAXED);
+    return RMDA_OK;
+}
+
+int rmda_moe_set_fused_combine(rmda_moe_ctx_t *ctx, int on) {
+    if (ctx == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    ctx->fused_combine = on != 0 ? 1 : 0;
     return RMDA_OK;
 }
 
@@ -841,6 +868,7 @@ static int gemm_pair(rmda_moe_ctx_t *ctx, hipStream_t s, rmda_gemm_args_t g, rmd
     if (tile_mode != 1u) {
         rmda_gemm_args_t h = g;
         h.n_items = n_items_hot;
+        h.fc = rmda_fc_t{};  // the compute tile leaves the combine to combine16_kernel
         const int rc = hip_check(ctx, rmda_launch_gemm_hot(s, &h, cfg.grid, ctx->hot_stages, ctx->hot_sched), what);
         if (rc != RMDA_OK || tile_mode == 2u) {
             return rc;
@@ -958,6 +986,10 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         }
         }
     }
+    // The combine folds into the down GEMM when the streaming tile runs it on
+    // packed weights; when the compute tile may run instead, combine16_kernel
+    // is enqueued too and does the combine only if that tile ran.
+    const bool fold_combine = ctx->fused_combine != 0 && packed != nullptr && ctx->g2.spec != 0 && tile_mode != 2u;
     // A2 counts, offsets, block bases and the GEMM work list
     bool self_perm = false;
     if (rc == RMDA_OK) {
@@ -985,6 +1017,15 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.shared_row0 = p.sh_row0;
         // all pairs in one rank block, or few enough pairs that every block
         // counts them all: the rank blocks write the permutation too
+        ra.topk = K;
+        if (fold_combine) {
+            ra.fc_cnt = at<uint32_t>(ws, p.fc_cnt);
+            ra.fc_nblk = d / RMDA_FC_COLS;
+            ra.fc_rows = T;
+            ra.fc_shared = shape->shared > 0 ? 1u : 0u;
+            ra.fc_zero_out = args->out;
+            ra.fc_d = d;
+        }
         self_perm = p.nblocks == 1 ||
                     (p.npairs <= RMDA_RANK_ALL_MAX && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0);
         if (self_perm) {
@@ -1063,6 +1104,20 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.inter = 0;
         g.out = ye;
         g.ldo = d;
+        if (fold_combine) {
+            g.fc.cnt = at<uint32_t>(ws, p.fc_cnt);
+            g.fc.nblk = d / RMDA_FC_COLS;
+            g.fc.rowtok = rowtok;
+            g.fc.slot = slot;
+            g.fc.wt = wt;
+            g.fc.proj = proj;
+            g.fc.pstride = p.ps;
+            g.fc.sg_off = E;
+            g.fc.topk = K;
+            g.fc.has_shared = shape->shared > 0 ? 1u : 0u;
+            g.fc.out = args->out;
+            g.fc.hc = rmda_hc_t{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
+        }
         rc = gemm_pair(ctx, s, g, ctx->g2, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), tile_mode,
                        "layer down");
     }
@@ -1071,14 +1126,16 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     }
     // A8/A9 combine (+ sigmoid-gated shared expert, + hyper-connection streams)
     const rmda_hc_t hcp{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
-    if (rc == RMDA_OK) {
+    if (rc == RMDA_OK && !(fold_combine && tile_mode == 1u)) {
         rc = hip_check(ctx,
                        rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.sh_row0, shape->shared > 0, args->out,
-                                             T, d, K, &hcp),
+                                             T, d, K, &hcp, fold_combine ? at<uint32_t>(ws, p.n_items_hot) : nullptr),
                        "layer combine");
-    }
-    if (rc == RMDA_OK) {
-        rc = prof_mark(ctx, RMDA_STAGE_COMBINE + 1);
+        if (rc == RMDA_OK) {
+            rc = prof_mark(ctx, RMDA_STAGE_COMBINE + 1);
+        }
+    } else if (rc == RMDA_OK) {
+        prof_skip(ctx, RMDA_STAGE_COMBINE);
     }
     if (rc == RMDA_OK && ctx->prof_on) {
         ctx->prof_pending += 1;

@@ -18,7 +18,7 @@
 namespace {
 
 __device__ __forceinline__ float sigmoidf(float v) {
-    return 1.0f / (1.0f + expf(-v));
+    return rmda_sigmoidf(v);
 }
 
 __global__ __launch_bounds__(256) void combine_ref_kernel(rmda_pc_moe_combine_t pc,
@@ -141,7 +141,11 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
                                                         uint32_t pstride, uint32_t sg_off,
                                                         uint32_t shared_row0, int has_shared,
                                                         uint16_t *__restrict__ out, uint32_t d,
-                                                        uint32_t topk, rmda_hc_t hcp) {
+                                                        uint32_t topk, rmda_hc_t hcp,
+                                                        const uint32_t *__restrict__ run_if) {
+    if (run_if != nullptr && *run_if == 0) {
+        return;  // the down GEMM folded the combine in
+    }
     __shared__ uint32_t s_slot[RMDA_MAX_TOPK + 1];
     __shared__ float s_wt[RMDA_MAX_TOPK + 1];
     __shared__ float s_g[RMDA_MAX_HC];
@@ -171,48 +175,18 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
             if (s == RMDA_NONE) {
                 continue;
             }
-            const float wj = s_wt[j];
-            const uint4 q = reinterpret_cast<const uint4 *>(y + (size_t)s * d)[c];
-            const uint16_t *hv = reinterpret_cast<const uint16_t *>(&q);
-#pragma unroll
-            for (int v = 0; v < 8; v += 1) {
-                acc[v] += wj * rmda_h2f(hv[v]);
-            }
+            rmda_comb_acc8(acc, s_wt[j], reinterpret_cast<const uint4 *>(y + (size_t)s * d)[c]);
         }
         if (has_shared) {
-            const float wj = s_wt[RMDA_MAX_TOPK];
-            const uint4 q = reinterpret_cast<const uint4 *>(y + (size_t)s_slot[RMDA_MAX_TOPK] * d)[c];
-            const uint16_t *hv = reinterpret_cast<const uint16_t *>(&q);
-#pragma unroll
-            for (int v = 0; v < 8; v += 1) {
-                acc[v] += wj * rmda_h2f(hv[v]);
-            }
+            rmda_comb_acc8(acc, s_wt[RMDA_MAX_TOPK],
+                           reinterpret_cast<const uint4 *>(y + (size_t)s_slot[RMDA_MAX_TOPK] * d)[c]);
         }
         if (out != nullptr) {
-            uint4 o;
-            uint16_t *ov = reinterpret_cast<uint16_t *>(&o);
-#pragma unroll
-            for (int v = 0; v < 8; v += 1) {
-                ov[v] = rmda_f2h(acc[v]);
-            }
-            reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = o;
+            reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = rmda_pack8_f16(acc);
         }
         if (HC) {
             for (uint32_t st = 0; st < hcp.hc; st += 1) {
-                float4 *hp = reinterpret_cast<float4 *>(hcp.h + ((size_t)r * hcp.hc + st) * d + (size_t)c * 8);
-                const float g = s_g[st];
-                float4 a = hp[0];
-                float4 b = hp[1];
-                a.x += acc[0] * g;
-                a.y += acc[1] * g;
-                a.z += acc[2] * g;
-                a.w += acc[3] * g;
-                b.x += acc[4] * g;
-                b.y += acc[5] * g;
-                b.z += acc[6] * g;
-                b.w += acc[7] * g;
-                hp[0] = a;
-                hp[1] = b;
+                rmda_hc_acc8(hcp.h + ((size_t)r * hcp.hc + st) * d + (size_t)c * 8, acc, s_g[st]);
             }
         }
     }
@@ -250,16 +224,16 @@ hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t 
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
                                  uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
-                                 const rmda_hc_t *hc) {
+                                 const rmda_hc_t *hc, const uint32_t *run_if) {
     if (rows == 0) {
         return hipSuccess;
     }
     if (hc != nullptr && hc->h != nullptr) {
         hipLaunchKernelGGL(combine16_kernel<true>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride, sg_off,
-                           shared_row0, has_shared, out, d, topk, *hc);
+                           shared_row0, has_shared, out, d, topk, *hc, run_if);
     } else {
         hipLaunchKernelGGL(combine16_kernel<false>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride,
-                           sg_off, shared_row0, has_shared, out, d, topk, rmda_hc_t{});
+                           sg_off, shared_row0, has_shared, out, d, topk, rmda_hc_t{}, run_if);
     }
     return hipGetLastError();
 }

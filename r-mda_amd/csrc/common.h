@@ -27,6 +27,50 @@ __device__ __forceinline__ uint32_t rmda_load_agent(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ float rmda_sigmoidf(float v) {
+    return 1.0f / (1.0f + expf(-v));
+}
+
+// One combine term over 8 consecutive columns: acc[v] += w * y[v] for the
+// 8 fp16 values in q, as one fused multiply-add each.  The fused layer's
+// combine kernel and the down GEMM's folded-in combine both sum through this,
+// so their outputs agree bit for bit.
+__device__ __forceinline__ void rmda_comb_acc8(float acc[8], float w, uint4 q) {
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int v = 0; v < 4; v += 1) {
+        acc[2 * v] = __builtin_fmaf(w, rmda_h2f((uint16_t)(u[v] & 0xffffu)), acc[2 * v]);
+        acc[2 * v + 1] = __builtin_fmaf(w, rmda_h2f((uint16_t)(u[v] >> 16)), acc[2 * v + 1]);
+    }
+}
+
+// The hyper-connection update of one token's 8 columns in one stream:
+// h[c + v] += acc[v] * gate (gate = 2 * sigmoid(inj / hc)), h 16-byte aligned.
+__device__ __forceinline__ void rmda_hc_acc8(float *h, const float acc[8], float gate) {
+    float4 *hp = reinterpret_cast<float4 *>(h);
+    float4 a = hp[0];
+    float4 b = hp[1];
+    a.x = __builtin_fmaf(acc[0], gate, a.x);
+    a.y = __builtin_fmaf(acc[1], gate, a.y);
+    a.z = __builtin_fmaf(acc[2], gate, a.z);
+    a.w = __builtin_fmaf(acc[3], gate, a.w);
+    b.x = __builtin_fmaf(acc[4], gate, b.x);
+    b.y = __builtin_fmaf(acc[5], gate, b.y);
+    b.z = __builtin_fmaf(acc[6], gate, b.z);
+    b.w = __builtin_fmaf(acc[7], gate, b.w);
+    hp[0] = a;
+    hp[1] = b;
+}
+
+__device__ __forceinline__ uint4 rmda_pack8_f16(const float acc[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int v = 0; v < 4; v += 1) {
+        u[v] = (uint32_t)rmda_f2h(acc[2 * v]) | ((uint32_t)rmda_f2h(acc[2 * v + 1]) << 16);
+    }
+    return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
 // Order-preserving map of a non-NaN float to uint32 (-0 and +0 map equal).
 __device__ __forceinline__ uint32_t rmda_float_key(float v) {
     uint32_t u = __builtin_bit_cast(uint32_t, v);
@@ -246,6 +290,16 @@ struct rmda_rank_args_t {
     // count/off/the work list, and hist/done are not used.  O(npairs) L2
     // reads per block: for npairs <= RMDA_RANK_ALL_MAX; idx 16-byte aligned.
     uint32_t count_all;
+    // folded combine (optional): fc_cnt[t][b] = has_shared + the number of
+    // selectable pairs of token t, for every b < fc_nblk; a token with no
+    // rows at all gets a zero row in fc_zero_out (when not NULL), the value
+    // the combine would write.  idx holds fc_rows * topk pairs.
+    uint32_t *fc_cnt;
+    uint32_t fc_nblk;
+    uint32_t fc_rows;
+    uint32_t fc_shared;
+    uint16_t *fc_zero_out;
+    uint32_t fc_d;
 };
 #define RMDA_RANK_ALL_MAX (1u << 16)
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);
@@ -274,6 +328,39 @@ enum {
     RMDA_GEMM_F16 = 1,    // down: A rows direct, out fp16
     RMDA_GEMM_F32 = 2     // reference matmul_f16_moe: A rows direct, out fp32 * scale
 };
+// hyper-connection epilogue of the fused combine (h == NULL: none)
+struct rmda_hc_t {
+    float *h;
+    const float *inj;
+    uint32_t inj_stride;
+    uint32_t inj_off;
+    uint32_t hc;
+};
+#define RMDA_MAX_HC 8u
+
+// The combine folded into the down GEMM (F16 mode, streaming tile).  cnt
+// holds one arrival counter per (token, 64 output columns), preset by the
+// rank kernel to the number of rows the token sends through the down GEMM
+// (its selected experts, plus the shared expert's row).  A wave that has
+// stored its 64 columns of a row takes one from the row's counter; the wave
+// that takes the last one sums the token's rows for those 64 columns in j
+// order, then the sigmoid-gated shared row, as the combine kernel does.
+#define RMDA_FC_COLS 64u
+struct rmda_fc_t {
+    uint32_t *cnt;           // [rows][nblk], or NULL: no folded combine
+    uint32_t nblk;           // d / RMDA_FC_COLS
+    const uint32_t *rowtok;  // sorted row -> token (routed rows)
+    const uint32_t *slot;    // [rows][topk]
+    const float *wt;         // [rows][topk]
+    const float *proj;       // router logits: the shared gate at [r * pstride + sg_off]
+    uint32_t pstride;
+    uint32_t sg_off;
+    uint32_t topk;
+    uint32_t has_shared;
+    uint16_t *out;           // [rows][d] fp16, or NULL
+    rmda_hc_t hc;            // hc.h != NULL: hyper-connection streams
+};
+
 struct rmda_gemm_args_t {
     int mode;
     const uint16_t *a;        // A base
@@ -296,6 +383,7 @@ struct rmda_gemm_args_t {
     const uint32_t *tiles;    // F32 mode: reference tile map instead of items
     const uint32_t *amax;
     uint32_t sa, sb;
+    rmda_fc_t fc;             // F16 mode: the folded-in combine (fc.cnt == NULL: none)
 };
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 // gemm_ref.hip: the F32 (reference matmul_f16_moe) contract on the
@@ -356,20 +444,14 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
                                const uint32_t *slot, const float *y, const float *proj,
                                const float *sh, const float *inj, float *h, uint16_t *out);
 // fused-layer combine: y fp16 rows, optional shared rows at shared_row0 + r.
-// hyper-connection epilogue of the fused combine (h == NULL: none)
-struct rmda_hc_t {
-    float *h;
-    const float *inj;
-    uint32_t inj_stride;
-    uint32_t inj_off;
-    uint32_t hc;
-};
-#define RMDA_MAX_HC 8u
+// run_if (or NULL): the kernel returns at once unless *run_if != 0 (the
+// layer passes the compute tile's item count when the down GEMM may have
+// folded the combine in)
 hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
                                  uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
-                                 const rmda_hc_t *hc);
+                                 const rmda_hc_t *hc, const uint32_t *run_if);
 
 // elem.hip
 hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y);

@@ -439,6 +439,91 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     }
 }
 
+// Folded combine (rmda_fc_t), one token's 8 columns [col, col + 8): its
+// selected rows in j order, then the sigmoid-gated shared row, summed exactly
+// as combine16_kernel sums them.  The rows were stored by other waves, maybe
+// on other XCDs, with device-scope stores: they are read at device scope.
+__device__ __forceinline__ uint4 fc_load16(const uint16_t *p) {
+    const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+
+__device__ __forceinline__ void fc_combine8(const rmda_gemm_args_t &g, const uint16_t *ye, uint32_t tk, uint32_t col) {
+    const rmda_fc_t &f = g.fc;
+    const uint32_t d = g.n_w;
+    float acc[8];
+#pragma unroll
+    for (int v = 0; v < 8; v += 1) {
+        acc[v] = 0.0f;
+    }
+    for (uint32_t j = 0; j < f.topk; j += 1) {
+        const uint32_t s = f.slot[(size_t)tk * f.topk + j];
+        if (s == RMDA_NONE) {
+            continue;
+        }
+        rmda_comb_acc8(acc, f.wt[(size_t)tk * f.topk + j], fc_load16(ye + (size_t)s * g.ldo + col));
+    }
+    if (f.has_shared) {
+        rmda_comb_acc8(acc, rmda_sigmoidf(f.proj[(size_t)tk * f.pstride + f.sg_off]),
+                       fc_load16(ye + (size_t)(g.shared_row0 + tk) * g.ldo + col));
+    }
+    if (f.out != nullptr) {
+        *reinterpret_cast<uint4 *>(f.out + (size_t)tk * d + col) = rmda_pack8_f16(acc);
+    }
+    if (f.hc.h != nullptr) {
+        for (uint32_t st = 0; st < f.hc.hc; st += 1) {
+            const float gate =
+                2.0f * rmda_sigmoidf(f.hc.inj[(size_t)tk * f.hc.inj_stride + f.hc.inj_off + st] / (float)f.hc.hc);
+            rmda_hc_acc8(f.hc.h + ((size_t)tk * f.hc.hc + st) * d + col, acc, gate);
+        }
+    }
+}
+
+// The arrival step, run by one MFMA wave right after it stored columns
+// [cb * 64, cb * 64 + 64) of its 64 rows of a task (rows [row0, row0 + rows)
+// of the sorted row space; lane l holds tile row r = the wave's first row + l).
+// Ordering: the wave's device-scope ye stores are acknowledged at the device
+// coherence point before s_waitcnt vmcnt(0) lets the counter decrements issue
+// (the MFMA waves have no other vector-memory operations outstanding), so a
+// wave that sees a counter reach zero issues its device-scope loads only after
+// every row of that counter was stored and acknowledged.  No fence: an
+// agent-scope release/acquire would write back and invalidate this XCD's
+// whole L2 on every task.
+__device__ __forceinline__ void fc_arrive(const rmda_gemm_args_t &g, const uint16_t *ye, uint32_t row0, uint32_t rows,
+                                          bool shared, uint32_t cb, uint32_t r, uint32_t lane, uint32_t *list) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const rmda_fc_t &f = g.fc;
+    bool last = false;
+    uint32_t t = 0;
+    if (r < rows) {
+        const uint32_t row = row0 + r;
+        t = shared ? row - g.shared_row0 : f.rowtok[row];
+        last = __hip_atomic_fetch_sub(&f.cnt[(size_t)t * f.nblk + cb], 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == 1u;
+    }
+    const uint64_t mask = __ballot(last);
+    if (mask == 0) {
+        return;
+    }
+    // the tokens this wave completes, compacted into its LDS list
+    const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+    if (last) {
+        list[pos] = t;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // 8 lanes per token, 8 columns (16 bytes) per lane, 8 tokens at a time
+    const uint32_t n = (uint32_t)__popcll(mask);
+    const uint32_t q = lane / 8;
+    const uint32_t col = cb * RMDA_FC_COLS + (lane % 8) * 8;
+    for (uint32_t b0 = 0; b0 < n; b0 += 8) {
+        if (b0 + q < n) {
+            fc_combine8(g, ye, list[b0 + q], col);
+        }
+    }
+}
+
 // Dedicated-issue variant: the 12 MFMA waves issue no loads; NDW more waves
 // issue every stage's DMA (A rows and packed B slabs) and do nothing else.
 // Each stage: the issue waves wait for their loads of stage g (exact vmcnt:
@@ -447,7 +532,12 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
 // the buffer stage g - 1 used while the MFMA waves multiply stage g.  So a
 // stage's loads go out right after the barrier instead of between MFMA
 // groups, and no MFMA wave waits on vmcnt.  Packed weights only.
-template <int MODE, int STAGES, int BPOL, int NDW, bool DB>
+//
+// FC (F16 mode): the combine folded in (rmda_fc_t).  The MFMA waves store
+// their ye tile with device-scope stores, wait for them, take one from the
+// arrival counter of each stored row's (token, 64 columns), and the wave that
+// takes a counter's last one sums that token's rows for its 64 columns.
+template <int MODE, int STAGES, int BPOL, int NDW, bool DB, bool FC = false>
 __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t BN = 256;
     constexpr uint32_t BK = 32;
@@ -467,7 +557,9 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     static_assert(AROWS <= 48, "gathered rows per issue wave");
     constexpr uint32_t A_STEP = MODE == RMDA_GEMM_F16 ? RMDA_HP_ROWS * BK : BK;  // hp is in 16 x 32 blocks
     static_assert((NMW + NDW) * RMDA_WAVE <= 1024, "workgroup size");
+    static_assert(!FC || MODE == RMDA_GEMM_F16, "the combine folds into the down GEMM only");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+    __shared__ uint32_t fc_list[FC ? NMW * RMDA_WAVE : 1];  // per MFMA wave: tokens whose counter it emptied
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
@@ -608,6 +700,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     uint32_t c_row0 = 0;
     uint32_t c_rows = 0;
     uint32_t c_nt = 0;
+    bool c_shared = false;
     uint32_t kc = 0;
     uint32_t ks = 0;
     bool live = false;
@@ -630,6 +723,9 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             const uint32_t item = sched.item(kc, c_nt);
             c_row0 = items[item * 4 + 1];
             c_rows = items[item * 4 + 2];
+            if (FC) {
+                c_shared = items[item * 4 + 0] == g.shared_group;
+            }
             live = wm * 64 < c_rows;
             nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
 #pragma unroll
@@ -661,10 +757,22 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
 #pragma unroll
                             for (int j = 0; j < 4; j += 1) {
                                 const uint32_t col = c_nt * BN + wn * 64 + j * 16 + fr;
-                                O[(size_t)(c_row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
+                                uint16_t *dst = &O[(size_t)(c_row0 + rr) * g.ldo + col];
+                                if (FC) {
+                                    // through to the device coherence point: the
+                                    // token's combine may run on another XCD
+                                    __hip_atomic_store(dst, rmda_f2h(acc[i][j][v]), __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+                                } else {
+                                    *dst = rmda_f2h(acc[i][j][v]);
+                                }
                             }
                         }
                     }
+                }
+                if (FC) {
+                    fc_arrive(g, O, c_row0, c_rows, c_shared, c_nt * (BN / RMDA_FC_COLS) + wn, wm * 64 + lane, lane,
+                              fc_list + w * RMDA_WAVE);
                 }
             } else {
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
@@ -1022,12 +1130,23 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
             hipLaunchKernelGGL((gemm4_kernel<5, 2, 4>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
             return hipGetLastError();
         }
+        if (a->fc.cnt != nullptr) {
+            if (MODE != RMDA_GEMM_F16 || c.spec == 5 || a->n_w % RMDA_FC_COLS != 0) {
+                return hipErrorInvalidValue;
+            }
+            hipLaunchKernelGGL((gemm3_kernel<RMDA_GEMM_F16, 5, 2, 4, false, true>), grid, dim3(16 * RMDA_WAVE), 0,
+                               s, *a);
+            return hipGetLastError();
+        }
         if (c.spec == 5 || ((c.spec == 6 || c.spec == 7) && MODE == RMDA_GEMM_SWIGLU)) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
         } else {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
         }
         return hipGetLastError();
+    }
+    if (a->fc.cnt != nullptr) {
+        return hipErrorInvalidValue;  // the folded combine runs on the dedicated-issue kernel only
     }
     if (c.stages == 4) {
         return launch_cfg<MODE, 256, 32, 4, 2>(s, a, grid, packed);

@@ -130,6 +130,32 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         pre[e] = 0;
         post[e] = 0;
     }
+    // Folded combine: preset each token's arrival counters to the number of
+    // rows it sends through the down GEMM.  Block b takes the tokens whose
+    // first pair lies in its own 1024 pairs (so their idx words are mostly the
+    // ones this block loads below); a token with no rows at all gets the zero
+    // output row the combine would have written.
+    if (a.fc_cnt != nullptr) {
+        const uint32_t K = a.topk;
+        const uint32_t t_lo = (b * RMDA_RANK_BLOCK + K - 1) / K;
+        const uint32_t t_hi = min(((b + 1) * RMDA_RANK_BLOCK + K - 1) / K, a.fc_rows);
+        for (uint32_t t = t_lo + tid; t < t_hi; t += NT) {
+            uint32_t n = a.fc_shared;
+            for (uint32_t j = 0; j < K; j += 1) {
+                n += a.idx[(size_t)t * K + j] < E ? 1u : 0u;
+            }
+            uint4 *c4 = reinterpret_cast<uint4 *>(a.fc_cnt + (size_t)t * a.fc_nblk);
+            for (uint32_t q = 0; q < a.fc_nblk / 4; q += 1) {
+                c4[q] = make_uint4(n, n, n, n);
+            }
+            if (n == 0 && a.fc_zero_out != nullptr) {
+                uint4 *o4 = reinterpret_cast<uint4 *>(a.fc_zero_out + (size_t)t * a.fc_d);
+                for (uint32_t q = 0; q < a.fc_d / 8; q += 1) {
+                    o4[q] = make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+        }
+    }
     // count_all: the other blocks' pairs as 16-byte words, CB per thread per
     // batch; the first batch is issued now and lands during the ranking
     // below (idx was written on other XCDs, so these loads miss L2)

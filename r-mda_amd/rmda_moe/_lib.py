@@ -119,6 +119,7 @@ SIGNATURES = {
     "rmda_moe_set_stream": (ctypes.c_int, [_p, _p]),
     "rmda_moe_set_hot_rows": (ctypes.c_int, [_p, _u32]),
     "rmda_moe_set_tile_policy": (ctypes.c_int, [_p, ctypes.c_int]),
+    "rmda_moe_set_fused_combine": (ctypes.c_int, [_p, ctypes.c_int]),
     "rmda_moe_ctx_error": (ctypes.c_int, [_p]),
     "rmda_moe_ctx_message": (ctypes.c_char_p, [_p]),
     "rmda_moe_ctx_clear_error": (None, [_p]),

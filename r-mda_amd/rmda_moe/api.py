@@ -111,6 +111,10 @@ class Context:
         """rmda_moe_set_tile_policy (TILE_ADAPTIVE, TILE_AUTO, TILE_STREAM, TILE_HOT)."""
         self._check(self.L.rmda_moe_set_tile_policy(self.h, int(policy)))
 
+    def set_fused_combine(self, on):
+        """rmda_moe_set_fused_combine: fold the combine into the down GEMM."""
+        self._check(self.L.rmda_moe_set_fused_combine(self.h, 1 if on else 0))
+
     def _check(self, rc):
         if rc != 0:
             msg = self.L.rmda_moe_ctx_message(self.h)
