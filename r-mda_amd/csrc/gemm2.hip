@@ -524,6 +524,19 @@ __device__ __forceinline__ void fc_arrive(const rmda_gemm_args_t &g, const uint1
     }
 }
 
+// One task's work item as the MFMA waves need it (scalar loads).
+struct task_desc_t {
+    uint32_t grp, row0, rows, nt;
+};
+__device__ __forceinline__ task_desc_t task_desc(const task_sched_t &sched, const_u32p items, uint32_t q) {
+    task_desc_t t;
+    const uint32_t item = sched.item(q, t.nt);
+    t.grp = items[item * 4 + 0];
+    t.row0 = items[item * 4 + 1];
+    t.rows = items[item * 4 + 2];
+    return t;
+}
+
 // Dedicated-issue variant: the 12 MFMA waves issue no loads; NDW more waves
 // issue every stage's DMA (A rows and packed B slabs) and do nothing else.
 // Each stage: the issue waves wait for their loads of stage g (exact vmcnt:
@@ -706,25 +719,19 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     bool live = false;
     uint32_t nlive = 0;
     uint32_t cbuf = 0;
+    // the next task's descriptor, read one stage before its first K step, so
+    // that step's fragment reads already know which row groups are live
+    task_desc_t nx = task_desc(sched, items, 0u);
     for (uint32_t gs = 0; gs < nstage; gs += 1) {
         lds_barrier();
         const uint8_t *base = smem + cbuf * STAGE_BYTES;
         cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
-        half8_t fa[4], fb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i += 1) {
-            fa[i] = *reinterpret_cast<const half8_t *>(base + a_row_off + i * 16 * (BK * 2) + ch_off);
-            fb[i] = *reinterpret_cast<const half8_t *>(base + b_row_off + i * 16 * (BK * 2) + ch_off);
-        }
-        if (DB) {
-            lds_barrier();  // this stage's buffer is in registers: the issue waves may refill it
-        }
         if (ks == 0) {
-            const uint32_t item = sched.item(kc, c_nt);
-            c_row0 = items[item * 4 + 1];
-            c_rows = items[item * 4 + 2];
+            c_row0 = nx.row0;
+            c_rows = nx.rows;
+            c_nt = nx.nt;
             if (FC) {
-                c_shared = items[item * 4 + 0] == g.shared_group;
+                c_shared = nx.grp == g.shared_group;
             }
             live = wm * 64 < c_rows;
             nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
@@ -735,6 +742,27 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                     acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
                 }
             }
+        }
+        // a wave whose rows all lie past the item reads no fragments
+        half8_t fa[4], fb[4];
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+                fa[i] = *reinterpret_cast<const half8_t *>(base + a_row_off + i * 16 * (BK * 2) + ch_off);
+                fb[i] = *reinterpret_cast<const half8_t *>(base + b_row_off + i * 16 * (BK * 2) + ch_off);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+                fa[i] = half8_t{};
+                fb[i] = half8_t{};
+            }
+        }
+        if (DB) {
+            lds_barrier();  // this stage's buffer is in registers: the issue waves may refill it
+        }
+        if (ks == steps - 1 && kc + 1 < ntask) {
+            nx = task_desc(sched, items, kc + 1);
         }
 #pragma unroll
         for (int i = 0; i < 4; i += 1) {
@@ -1002,6 +1030,8 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
     uint32_t nlive = 0;
     uint32_t cbuf = 0;
     uint32_t abuf = 0;
+    // the next task's descriptor, read one stage before its first K step
+    task_desc_t nx = task_desc(sched, items, 0u);
     for (uint32_t gs = 0; gs < nstage; gs += 1) {
         lds_barrier();
         const uint8_t *bb = bring + cbuf * B_BYTES + b_off;
@@ -1010,17 +1040,10 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
         if ((gs & 1u) != 0) {
             abuf = abuf + 1 == A_SLOTS ? 0 : abuf + 1;
         }
-        half8_t fa[4], fb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i += 1) {
-            fa[i] = *reinterpret_cast<const half8_t *>(ab + i * 16 * (AK * 2));
-            fb[i] = *reinterpret_cast<const half8_t *>(bb + i * 16 * (BK * 2));
-        }
-        lds_barrier();  // both buffers are in registers: the issue waves may refill them
         if (ks == 0) {
-            const uint32_t item = sched.item(kc, c_nt);
-            c_row0 = items[item * 4 + 1];
-            c_rows = items[item * 4 + 2];
+            c_row0 = nx.row0;
+            c_rows = nx.rows;
+            c_nt = nx.nt;
             live = wm * 64 < c_rows;
             nlive = live ? min(4u, (c_rows - wm * 64 + 15) / 16) : 0u;
 #pragma unroll
@@ -1030,6 +1053,25 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
                     acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
                 }
             }
+        }
+        // a wave whose rows all lie past the item reads no fragments
+        half8_t fa[4], fb[4];
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+                fa[i] = *reinterpret_cast<const half8_t *>(ab + i * 16 * (AK * 2));
+                fb[i] = *reinterpret_cast<const half8_t *>(bb + i * 16 * (BK * 2));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i += 1) {
+                fa[i] = half8_t{};
+                fb[i] = half8_t{};
+            }
+        }
+        lds_barrier();  // both buffers are in registers: the issue waves may refill them
+        if (ks == steps - 1 && kc + 1 < ntask) {
+            nx = task_desc(sched, items, kc + 1);
         }
 #pragma unroll
         for (int i = 0; i < 4; i += 1) {
