@@ -961,8 +961,11 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_ROUTER + 1);
     }
-    // A1 top-k (unless fused above)
-    if (rc == RMDA_OK && !fuse_route) {
+    // A1 top-k (unless fused above).  When every pair fits one rank block
+    // (decode sizes), the rank kernel routes the rows itself, so the chain
+    // before gate_up is two launches (router, rank) instead of three.
+    const bool route_in_rank = !fuse_route && p.nblocks == 1;
+    if (rc == RMDA_OK && !fuse_route && !route_in_rank) {
         rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
         if (rc == RMDA_OK) {
             rc = prof_mark(ctx, RMDA_STAGE_ROUTE + 1);
@@ -1018,6 +1021,13 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         // all pairs in one rank block, or few enough pairs that every block
         // counts them all: the rank blocks write the permutation too
         ra.topk = K;
+        if (route_in_rank) {
+            ra.route_proj = proj;
+            ra.route_rows = T;
+            ra.route_stride = p.ps;
+            ra.route_idx = idx;
+            ra.route_wt = wt;
+        }
         if (fold_combine) {
             ra.fc_cnt = at<uint32_t>(ws, p.fc_cnt);
             ra.fc_nblk = d / RMDA_FC_COLS;

@@ -146,8 +146,9 @@ __device__ __forceinline__ void rmda_route_load(const float *l, uint32_t experts
 
 // The selection rounds of rmda_route_row on values already in registers
 // (lane l holds columns l, l+64, ...).  sel_row, when not NULL, receives the
-// selected columns as well (e.g. an LDS copy for the caller's next step).
-template <int NV>
+// selected columns as well (e.g. an LDS copy for the caller's next step);
+// AGENT_IDX stores idx_row at device scope.
+template <int NV, bool AGENT_IDX = false>
 __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t topk, uint32_t *idx_row,
                                                   float *wt_row, uint32_t *count, uint32_t *sel_row) {
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
@@ -192,7 +193,12 @@ __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t
         }
     }
     if (lane < topk) {
-        idx_row[lane] = my_sel;
+        if (AGENT_IDX) {
+            // read back by another workgroup of the same launch
+            __hip_atomic_store(&idx_row[lane], my_sel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            idx_row[lane] = my_sel;
+        }
         wt_row[lane] = expf(my_val - sv0) / z;
         if (sel_row != nullptr) {
             sel_row[lane] = my_sel;
@@ -300,6 +306,15 @@ struct rmda_rank_args_t {
     uint32_t fc_shared;
     uint16_t *fc_zero_out;
     uint32_t fc_d;
+    // top-k folded in (optional; npairs <= RMDA_RANK_BLOCK, done zero on
+    // entry): one block per 4 rows routes route_rows rows of logits
+    // (route_proj, row stride route_stride) as route_kernel does, into
+    // route_idx (which must be idx) and route_wt; the last of them ranks
+    const float *route_proj;
+    uint32_t route_rows;
+    uint32_t route_stride;
+    uint32_t *route_idx;
+    float *route_wt;
 };
 #define RMDA_RANK_ALL_MAX (1u << 16)
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a);

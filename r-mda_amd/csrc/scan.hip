@@ -2,8 +2,8 @@
 // permutation (the order moe_scatter's atomics would give if the pairs ran
 // one after another).
 //
-// rank_kernel: pairs are cut into blocks of RMDA_RANK_BLOCK.  A 256-thread
-// workgroup walks its block 256 pairs at a time; each wave ORs a 64-bit lane
+// rank_kernel: pairs are cut into blocks of RMDA_RANK_BLOCK.  A workgroup of
+// NT threads walks its block NT pairs at a time; each wave ORs a 64-bit lane
 // mask per expert in LDS, so a pair's rank among equal experts in its block
 // is (running count) + (masks of lower waves) + popcount(own mask & lanes
 // below).  The block's per-expert totals go to hist[b][e].  The last block to
@@ -19,7 +19,7 @@
 
 namespace {
 
-constexpr uint32_t NT0 = 256;  // threads of the helper kernels and of a multi-block rank launch
+constexpr uint32_t NT0 = 256;  // threads of the helper kernels and of a single-block rank launch
 
 __global__ __launch_bounds__(256) void zero_kernel(uint32_t *p, size_t n, uint32_t value) {
     for (size_t i = blockIdx.x * (size_t)NT0 + threadIdx.x; i < n; i += (size_t)gridDim.x * NT0) {
@@ -102,7 +102,9 @@ __global__ __launch_bounds__(512) void scan_kernel(const uint32_t *__restrict__ 
     }
 }
 
-template <uint32_t NT>
+// NV > 0: the top-k folded in (rmda_rank_args_t::route_proj), NV logits per
+// lane: one block per NT / 64 rows routes, and the last of them ranks.
+template <uint32_t NT, int NV>
 __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     __shared__ unsigned long long msk[NT / RMDA_WAVE][RMDA_MAX_EXPERTS];
     __shared__ uint32_t run[RMDA_MAX_EXPERTS];
@@ -117,8 +119,8 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = tid / RMDA_WAVE;
     const uint32_t E = a.experts;
-    const uint32_t b = blockIdx.x;
-    const uint32_t nb = gridDim.x;
+    const uint32_t b = NV > 0 ? 0u : blockIdx.x;  // routed: the ranking block stands for the one rank block
+    const uint32_t nb = NV > 0 ? 1u : gridDim.x;
     // every block counts every pair itself: no hand-off, and each block
     // writes its own slots (see rmda_rank_args_t::count_all)
     const bool all = a.count_all != 0 && nb > 1;
@@ -130,6 +132,42 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         pre[e] = 0;
         post[e] = 0;
     }
+    // Top-k folded in: block r's wave w routes row 4r + w as route_kernel
+    // does, storing its experts at device scope; the last block to finish
+    // (ticket) then ranks every pair as the single rank block, reading idx at
+    // device scope.  The other blocks leave.  Ordering without a fence: the
+    // device-scope idx stores are written through to the device coherence
+    // point and acknowledged before s_waitcnt vmcnt(0) lets the wave reach
+    // the barrier that precedes the ticket, and the last block's
+    // device-scope loads are issued after its ticket returned.
+    if constexpr (NV > 0) {
+        const uint32_t t = blockIdx.x * (NT / RMDA_WAVE) + w;
+        if (t < a.route_rows) {
+            float v[NV];
+            rmda_route_load<NV, false>(a.route_proj + (size_t)t * a.route_stride, E, v);
+            rmda_route_select<NV, true>(v, a.topk, a.route_idx + (size_t)t * a.topk, a.route_wt + (size_t)t * a.topk,
+                                        nullptr, nullptr);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            // the increment wraps the ticket back to 0 on the last block
+            s_last = __builtin_amdgcn_atomic_inc32(a.done, gridDim.x - 1, __ATOMIC_RELAXED, "agent") ==
+                     gridDim.x - 1;
+        }
+        __syncthreads();
+        if (!s_last) {
+            return;
+        }
+    }
+    // a pair's expert: written by other blocks of this launch when it routed
+    auto pair_expert = [&](uint32_t pr) -> uint32_t {
+        if constexpr (NV > 0) {
+            return rmda_load_agent(&a.idx[pr]);
+        } else {
+            return a.idx[pr];
+        }
+    };
     // Folded combine: preset each token's arrival counters to the number of
     // rows it sends through the down GEMM.  Block b takes the tokens whose
     // first pair lies in its own 1024 pairs (so their idx words are mostly the
@@ -142,7 +180,7 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         for (uint32_t t = t_lo + tid; t < t_hi; t += NT) {
             uint32_t n = a.fc_shared;
             for (uint32_t j = 0; j < K; j += 1) {
-                n += a.idx[(size_t)t * K + j] < E ? 1u : 0u;
+                n += pair_expert(t * K + j) < E ? 1u : 0u;
             }
             uint4 *c4 = reinterpret_cast<uint4 *>(a.fc_cnt + (size_t)t * a.fc_nblk);
             for (uint32_t q = 0; q < a.fc_nblk / 4; q += 1) {
@@ -198,7 +236,7 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
 #pragma unroll
     for (uint32_t it = 0; it < ITS; it += 1) {
         const uint32_t pr = b * RMDA_RANK_BLOCK + it * NT + tid;
-        ev[it] = pr < a.npairs ? a.idx[pr] : RMDA_NONE;
+        ev[it] = pr < a.npairs ? pair_expert(pr) : RMDA_NONE;
     }
 #pragma unroll
     for (uint32_t it = 0; it < ITS; it += 1) {
@@ -589,6 +627,34 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     if (nb == 0) {
         nb = 1;  // one block still finalises (zero counts, empty work list)
     }
-    hipLaunchKernelGGL((rank_kernel<NT0>), dim3(nb), dim3(NT0), 0, s, *a);
+    // one block (up to 1024 pairs): 256 threads; several blocks: 1024, one
+    // thread per pair, so each block ranks its pairs in one pass and spreads
+    // the per-expert finishing work over four times the threads (BASELINE
+    // config 5, 20 blocks over 512 experts: rank 15.5 -> 10.2 us; config 3
+    // 7.6 -> 7.35 us; one block is 0.15 us slower with 1024)
+    if (a->route_proj != nullptr) {
+        // top-k folded in: one block per 4 rows routes, the last one ranks
+        if (nb != 1 || a->experts > RMDA_MAX_EXPERTS || a->topk == 0 || a->done == nullptr ||
+            a->route_rows * a->topk != a->npairs) {
+            return hipErrorInvalidValue;
+        }
+        const uint32_t nv = (a->experts + RMDA_WAVE - 1) / RMDA_WAVE;
+        const dim3 g1((a->route_rows + NT0 / RMDA_WAVE - 1) / (NT0 / RMDA_WAVE)), b1(NT0);
+        if (nv <= 1) {
+            hipLaunchKernelGGL((rank_kernel<NT0, 1>), g1, b1, 0, s, *a);
+        } else if (nv <= 2) {
+            hipLaunchKernelGGL((rank_kernel<NT0, 2>), g1, b1, 0, s, *a);
+        } else if (nv <= 4) {
+            hipLaunchKernelGGL((rank_kernel<NT0, 4>), g1, b1, 0, s, *a);
+        } else {
+            hipLaunchKernelGGL((rank_kernel<NT0, RMDA_MAX_EXPERTS / RMDA_WAVE>), g1, b1, 0, s, *a);
+        }
+        return hipGetLastError();
+    }
+    if (nb > 1) {
+        hipLaunchKernelGGL((rank_kernel<1024, 0>), dim3(nb), dim3(1024), 0, s, *a);
+    } else {
+        hipLaunchKernelGGL((rank_kernel<NT0, 0>), dim3(nb), dim3(NT0), 0, s, *a);
+    }
     return hipGetLastError();
 }
