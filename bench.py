@@ -71,6 +71,8 @@ def parse_args():
                     help="skip the config-4 (skewed, compute tile) and config-5 lines added to the config-3 run")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing the reference-equivalent stage entry points (route, scan, scatter, combine)")
+    ap.add_argument("--dropin-only", action="store_true",
+                    help="time only the reference-equivalent stage entry points (config 3 inputs), for profiling")
     ap.add_argument("--transient", action="store_true",
                     help="before the warm-up, time each of the first 400 layer calls of this fresh process, "
                          "then 60 more after a 2 s idle (the GPU's warm-up transient)")
@@ -442,6 +444,11 @@ def main():
     ctx = api.Context(0)
     inp = inputs.make_inputs(ctx, cfg, seed=0)
     shape = inp["shape"]
+    if args.dropin_only:
+        d = measure_dropins(ctx, torch, inp)
+        ctx.close()
+        print(json.dumps({"dropin": d}), flush=True)
+        return
     ws = inputs.workspace_for(shape)
     out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
 
