@@ -1536,7 +1536,7 @@ namespace {
 
 struct ShimPlan {
     size_t x16, a16, p, idx, wt, count, off, fill, tiles, slot, xp, g, hp, hp16, ye;
-    size_t gs, hs, hs16, sh, tiles1, amax, total;
+    size_t gs, hs, hs16, sh, tiles1, amax, wr, total;
     uint32_t ps, rows_pad, mrows;
 };
 
@@ -1589,6 +1589,9 @@ ShimPlan plan_shim(const rmda_qwen_moe_t *q) {
         p.tiles1 = take((size_t)p.rows_pad / RMDA_QWEN_TILE * 4);
     }
     p.amax = take((size_t)RMDA_QWEN_MAX_SLOTS * 4);
+    // the router matrix in the packed order of the fused layer's router
+    // (repacked by every recording: 2 bytes of traffic per weight byte)
+    p.wr = take((size_t)d * rmda_router_cpad(p.ps) * 4);
     p.total = o;
     return p;
 }
@@ -1684,7 +1687,11 @@ int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const u
     return rmda_moe_mm(q->ctx, &pc, a, w, out, scr<uint32_t>(q, p.amax), scr<uint32_t>(q, p.tiles));
 }
 
-int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows) {
+namespace {
+
+// mda_qwen_route_rec's work; zero_xp = false leaves xp's padding rows as
+// they are, for the recording below, which reads no padding row's result
+int route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows, bool zero_xp) {
     ShimPlan p;
     int rc = shim_enter(q, "rmda_qwen_route_rec", &p);
     if (rc != RMDA_OK) {
@@ -1700,10 +1707,12 @@ int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows) {
     // the reference zero-fills xp (src/qwen.c:798); count, fill and the tile
     // map need no fill here (route overwrites count, scatter takes fill as
     // zero, scan writes every tile)
-    rc = hip_check(q->ctx, rmda_launch_zero(q->ctx->stream, scr<uint32_t>(q, p.xp), (size_t)mrows * q->d / 2, 0),
-                   "route_rec xp fill");
-    if (rc != RMDA_OK) {
-        return rc;
+    if (zero_xp) {
+        rc = hip_check(q->ctx, rmda_launch_zero(q->ctx->stream, scr<uint32_t>(q, p.xp), (size_t)mrows * q->d / 2, 0),
+                       "route_rec xp fill");
+        if (rc != RMDA_OK) {
+            return rc;
+        }
     }
     const rmda_pc_moe_route_t pr{rows, q->experts, q->topk, p.ps};
     rc = rmda_moe_route(q->ctx, &pr, scr<float>(q, p.p), scr<uint32_t>(q, p.idx), scr<float>(q, p.wt),
@@ -1723,6 +1732,12 @@ int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows) {
                               scr<uint32_t>(q, p.slot));
     }
     return rc;
+}
+
+}  // namespace
+
+int rmda_qwen_route_rec(rmda_qwen_moe_t *q, uint32_t rows, uint32_t mrows) {
+    return route_rec(q, rows, mrows, true);
 }
 
 int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, float *h, uint16_t *out,
@@ -1758,13 +1773,24 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
         const rmda_pc_cast_t pc{rows * d, RMDA_NO_SLOT};
         rc = rmda_cast_f16(c, &pc, x, scr<uint16_t>(q, p.x16), amax);
     }
+    // the router projection on the router matrix repacked into the order the
+    // router kernel streams (3.6 us for 128 x 2048 at config 3; the HF-layout
+    // kernel takes about three times as long as the packed one), the same
+    // logits bit for bit
     if (rc == RMDA_OK) {
-        const rmda_moe_router_t pr{rows, d, p.ps, p.ps, 0};
-        rc = rmda_moe_router(c, &pr, scr<uint16_t>(q, p.x16), q->w_router, nullptr, scr<float>(q, p.p));
+        rc = hip_check(c, rmda_launch_router_pack(c->stream, q->w_router, scr<float>(q, p.wr), p.ps, d),
+                       "moe_rec router pack");
     }
-    // A1-A3
     if (rc == RMDA_OK) {
-        rc = rmda_qwen_route_rec(q, rows, mrows);
+        rc = hip_check(c,
+                       rmda_launch_router(c->stream, scr<uint16_t>(q, p.x16), scr<float>(q, p.wr), 1, nullptr,
+                                          scr<float>(q, p.p), rows, d, p.ps, p.ps, 0, nullptr, 0, nullptr),
+                       "moe_rec router");
+    }
+    // A1-A3 (xp's padding rows are not zero-filled: the SwiGLU, absmax and
+    // cast below read the routed rows only)
+    if (rc == RMDA_OK) {
+        rc = route_rec(q, rows, mrows, false);
     }
     // A4-A7: gate_up, SwiGLU, hp cast with a slot, down (src/qwen.c:847-878)
     if (rc == RMDA_OK) {
@@ -1777,14 +1803,21 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
         sh = shim_slot(q);
         rc = sh == RMDA_NO_SLOT ? c->err : RMDA_OK;
     }
+    // over the rows that hold routed pairs only: the padding rows of each
+    // 128-row segment are zero in g (xp's zero rows), so their SwiGLU is 0 and
+    // leaves the absmax unchanged, and nothing after reads their hp or ye
+    const rmda_rowmask_t live{scr<uint32_t>(q, p.tiles), scr<uint32_t>(q, p.off), scr<uint32_t>(q, p.count),
+                              RMDA_QWEN_TILE};
     if (rc == RMDA_OK) {
         const rmda_pc_qwen_elem_t pe{mrows, I, 2 * I, 0, I, 0, 1.0f};
-        rc = hip_check(c, rmda_launch_elem_absmax(c->stream, &pe, scr<float>(q, p.g), scr<float>(q, p.hp), amax, sh),
+        rc = hip_check(c, rmda_launch_elem_absmax_rows(c->stream, &pe, scr<float>(q, p.g), scr<float>(q, p.hp), amax,
+                                                       sh, &live),
                        "moe_rec swiglu");
     }
     if (rc == RMDA_OK) {
-        const rmda_pc_cast_t pc{mrows * I, sh};
-        rc = rmda_cast_f16(c, &pc, scr<float>(q, p.hp), scr<uint16_t>(q, p.hp16), amax);
+        rc = hip_check(c, rmda_launch_cast_rows(c->stream, mrows, I, scr<float>(q, p.hp), scr<uint16_t>(q, p.hp16),
+                                                amax, sh, &live),
+                       "moe_rec hp cast");
     }
     if (rc == RMDA_OK) {
         rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.hp16), sh, q->w_down, scr<float>(q, p.ye), mrows, d, I);

@@ -475,6 +475,22 @@ hipError_t rmda_launch_absmax(hipStream_t s, const rmda_pc_absmax_t *pc, const f
 // rmda_launch_absmax would leave it over y)
 hipError_t rmda_launch_elem_absmax(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y,
                                    uint32_t *amax, uint32_t slot);
+// Rows of a P-padded permuted row space (moe_scan's segments) that hold
+// routed pairs: row r is live when e = tiles[r / tile] names an expert and
+// r - off[e] < count[e].  The recording's SwiGLU, absmax and cast skip the
+// padding rows with it (their absmax is 0, the zero rows' own value).
+struct rmda_rowmask_t {
+    const uint32_t *tiles;
+    const uint32_t *off;
+    const uint32_t *count;
+    uint32_t tile;
+};
+// elem op 0 + absmax, and the scaled cast, over the live rows only (other
+// rows of y / dst are left as they were); rows of whole float4s
+hipError_t rmda_launch_elem_absmax_rows(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y,
+                                        uint32_t *amax, uint32_t slot, const rmda_rowmask_t *mask);
+hipError_t rmda_launch_cast_rows(hipStream_t s, uint32_t rows, uint32_t n, const float *src, uint16_t *dst,
+                                 const uint32_t *amax, uint32_t slot, const rmda_rowmask_t *mask);
 hipError_t rmda_launch_cast(hipStream_t s, const rmda_pc_cast_t *pc, const float *src, uint16_t *dst,
                             const uint32_t *amax);
 hipError_t rmda_launch_bf16(hipStream_t s, uint32_t n, uint32_t *w);

@@ -102,6 +102,140 @@ __global__ __launch_bounds__(256) void cast_kernel(const float *__restrict__ src
     dst[i] = rmda_f2h(src[i] * cast_scale(amax, slot));
 }
 
+// 16-byte versions of elem_kernel, elem_absmax_kernel, absmax_kernel and
+// cast_kernel, for rows of whole float4s (n, astride, ao, bo multiples of 4,
+// buffers 16-byte aligned): the same expression per element, four elements
+// per lane, a block per (column range, row stride) so no index needs a
+// division.  The absmax kernels reduce per block and merge with one
+// atomicMax per block (at most 1024 blocks).
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
+__device__ __forceinline__ float silu_scaled1(float g, float scale) {
+    const float v = g * scale;
+    return v / (1.0f + expf(-v));
+}
+
+__device__ __forceinline__ void block_absmax(float m, uint32_t *amax, uint32_t slot) {
+    __shared__ float red[256];
+    const uint32_t tid = threadIdx.x;
+    red[tid] = m;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (tid < s) {
+            red[tid] = fmaxf(red[tid], red[tid + s]);
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        atomicMax(&amax[slot], __builtin_bit_cast(uint32_t, red[0]));
+    }
+}
+
+__device__ __forceinline__ bool row_live(const rmda_rowmask_t &mk, uint32_t r) {
+    const uint32_t e = mk.tiles[r / mk.tile];
+    return e != RMDA_NONE && r - mk.off[e] < mk.count[e];
+}
+
+template <bool ABS, bool MASK>
+__global__ __launch_bounds__(256) void elem4_kernel(rmda_pc_qwen_elem_t pc, const float *__restrict__ a,
+                                                    float *__restrict__ y, uint32_t *__restrict__ amax,
+                                                    uint32_t slot, rmda_rowmask_t mk) {
+    const uint32_t n4 = pc.n / 4;
+    float m = 0.0f;
+    for (uint32_t r = blockIdx.y; r < pc.rows; r += gridDim.y) {
+        if (MASK && !row_live(mk, r)) {
+            continue;
+        }
+        const float4 *ga = reinterpret_cast<const float4 *>(a + (size_t)r * pc.astride + pc.ao);
+        const float4 *ua = reinterpret_cast<const float4 *>(a + (size_t)r * pc.astride + pc.bo);
+        float4 *yr = reinterpret_cast<float4 *>(y + (size_t)r * pc.n);
+        for (uint32_t c = blockIdx.x * 256 + threadIdx.x; c < n4; c += gridDim.x * 256) {
+            const float4 g = ga[c];
+            float4 v;
+            if (pc.op == 0) {
+                const float4 u = ua[c];
+                v = make_float4(swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w));
+            } else {
+                v = make_float4(silu_scaled1(g.x, pc.scale), silu_scaled1(g.y, pc.scale),
+                                silu_scaled1(g.z, pc.scale), silu_scaled1(g.w, pc.scale));
+            }
+            yr[c] = v;
+            if (ABS) {
+                m = fmaxf(m, fabsf(v.x));
+                m = fmaxf(m, fabsf(v.y));
+                m = fmaxf(m, fabsf(v.z));
+                m = fmaxf(m, fabsf(v.w));
+            }
+        }
+    }
+    if (ABS) {
+        block_absmax(m, amax, slot);
+    }
+}
+
+__global__ __launch_bounds__(256) void absmax4_kernel(const float4 *__restrict__ x, uint32_t n4,
+                                                      uint32_t *__restrict__ amax, uint32_t slot) {
+    float m = 0.0f;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
+        const float4 v = x[i];
+        m = fmaxf(m, fabsf(v.x));
+        m = fmaxf(m, fabsf(v.y));
+        m = fmaxf(m, fabsf(v.z));
+        m = fmaxf(m, fabsf(v.w));
+    }
+    block_absmax(m, amax, slot);
+}
+
+template <bool MASK>
+__global__ __launch_bounds__(256) void cast4r_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                     uint32_t rows, uint32_t n, const uint32_t *__restrict__ amax,
+                                                     uint32_t slot, rmda_rowmask_t mk) {
+    const uint32_t n4 = n / 4;
+    const float sc = cast_scale(amax, slot);
+    for (uint32_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        if (MASK && !row_live(mk, r)) {
+            continue;
+        }
+        const float4 *sr = reinterpret_cast<const float4 *>(src + (size_t)r * n);
+        uint2 *dr = reinterpret_cast<uint2 *>(dst + (size_t)r * n);
+        for (uint32_t c = blockIdx.x * 256 + threadIdx.x; c < n4; c += gridDim.x * 256) {
+            const float4 v = sr[c];
+            dr[c] = make_uint2((uint32_t)rmda_f2h(v.x * sc) | ((uint32_t)rmda_f2h(v.y * sc) << 16),
+                               (uint32_t)rmda_f2h(v.z * sc) | ((uint32_t)rmda_f2h(v.w * sc) << 16));
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void cast4_kernel(const float4 *__restrict__ src, uint2 *__restrict__ dst,
+                                                    uint32_t n4, const uint32_t *__restrict__ amax, uint32_t slot) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) {
+        return;
+    }
+    const float sc = cast_scale(amax, slot);
+    const float4 v = src[i];
+    dst[i] = make_uint2((uint32_t)rmda_f2h(v.x * sc) | ((uint32_t)rmda_f2h(v.y * sc) << 16),
+                        (uint32_t)rmda_f2h(v.z * sc) | ((uint32_t)rmda_f2h(v.w * sc) << 16));
+}
+
+bool aligned16(const void *p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+bool elem_vec_ok(const rmda_pc_qwen_elem_t *pc, const float *a, const float *y) {
+    return pc->n % 4 == 0 && pc->astride % 4 == 0 && pc->ao % 4 == 0 && (pc->op != 0 || pc->bo % 4 == 0) &&
+           aligned16(a) && aligned16(y);
+}
+
+dim3 elem_grid(const rmda_pc_qwen_elem_t *pc) {
+    const uint32_t gx = (pc->n / 4 + 255) / 256;
+    uint32_t gy = 1024 / (gx > 1024 ? 1024 : gx);
+    gy = gy > pc->rows ? pc->rows : gy;
+    return dim3(gx > 1024 ? 1024 : gx, gy < 1 ? 1 : gy);
+}
+
 __global__ __launch_bounds__(256) void bf16_kernel(uint32_t *__restrict__ w, uint32_t n) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) {
@@ -146,6 +280,11 @@ hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const 
     if (n == 0) {
         return hipSuccess;
     }
+    if (elem_vec_ok(pc, a, y)) {
+        hipLaunchKernelGGL((elem4_kernel<false, false>), elem_grid(pc), dim3(256), 0, s, *pc, a, y, nullptr, 0u,
+                           rmda_rowmask_t{});
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(elem_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, *pc, a, y);
     return hipGetLastError();
 }
@@ -156,12 +295,52 @@ hipError_t rmda_launch_elem_absmax(hipStream_t s, const rmda_pc_qwen_elem_t *pc,
     if (n == 0) {
         return hipSuccess;
     }
+    if (pc->op == 0 && elem_vec_ok(pc, a, y)) {
+        hipLaunchKernelGGL((elem4_kernel<true, false>), elem_grid(pc), dim3(256), 0, s, *pc, a, y, amax, slot,
+                           rmda_rowmask_t{});
+        return hipGetLastError();
+    }
     const uint64_t blocks = (n + 255) / 256 > 1024 ? 1024 : (n + 255) / 256;
     hipLaunchKernelGGL(elem_absmax_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, *pc, a, y, amax, slot);
     return hipGetLastError();
 }
 
+hipError_t rmda_launch_elem_absmax_rows(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y,
+                                        uint32_t *amax, uint32_t slot, const rmda_rowmask_t *mask) {
+    if (pc->rows == 0 || pc->n == 0) {
+        return hipSuccess;
+    }
+    if (pc->op != 0 || !elem_vec_ok(pc, a, y) || mask == nullptr) {
+        return rmda_launch_elem_absmax(s, pc, a, y, amax, slot);
+    }
+    hipLaunchKernelGGL((elem4_kernel<true, true>), elem_grid(pc), dim3(256), 0, s, *pc, a, y, amax, slot, *mask);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_cast_rows(hipStream_t s, uint32_t rows, uint32_t n, const float *src, uint16_t *dst,
+                                 const uint32_t *amax, uint32_t slot, const rmda_rowmask_t *mask) {
+    if (rows == 0 || n == 0) {
+        return hipSuccess;
+    }
+    if (n % 4 != 0 || !aligned16(src) || (reinterpret_cast<uintptr_t>(dst) & 7u) != 0 || mask == nullptr) {
+        const rmda_pc_cast_t pc{rows * n, slot};
+        return rmda_launch_cast(s, &pc, src, dst, amax);
+    }
+    rmda_pc_qwen_elem_t shape{};
+    shape.rows = rows;
+    shape.n = n;
+    hipLaunchKernelGGL((cast4r_kernel<true>), elem_grid(&shape), dim3(256), 0, s, src, dst, rows, n, amax, slot, *mask);
+    return hipGetLastError();
+}
+
 hipError_t rmda_launch_absmax(hipStream_t s, const rmda_pc_absmax_t *pc, const float *x, uint32_t *amax) {
+    if (pc->n % 4 == 0 && pc->n > 0 && aligned16(x)) {
+        uint32_t b4 = (pc->n / 4 + 255) / 256;
+        b4 = b4 > 1024 ? 1024 : b4;
+        hipLaunchKernelGGL(absmax4_kernel, dim3(b4), dim3(256), 0, s, reinterpret_cast<const float4 *>(x), pc->n / 4,
+                           amax, pc->slot);
+        return hipGetLastError();
+    }
     uint32_t blocks = (pc->n + 255) / 256;
     blocks = blocks < 1 ? 1 : (blocks > 1024 ? 1024 : blocks);
     hipLaunchKernelGGL(absmax_kernel, dim3(blocks), dim3(256), 0, s, x, pc->n, amax, pc->slot);
@@ -172,6 +351,12 @@ hipError_t rmda_launch_cast(hipStream_t s, const rmda_pc_cast_t *pc, const float
                             const uint32_t *amax) {
     if (pc->n == 0) {
         return hipSuccess;
+    }
+    if (pc->n % 4 == 0 && aligned16(src) && (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+        hipLaunchKernelGGL(cast4_kernel, dim3((pc->n / 4 + 255) / 256), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(src), reinterpret_cast<uint2 *>(dst), pc->n / 4, amax,
+                           pc->slot);
+        return hipGetLastError();
     }
     hipLaunchKernelGGL(cast_kernel, dim3((pc->n + 255) / 256), dim3(256), 0, s, src, dst, pc->n, amax, pc->slot);
     return hipGetLastError();

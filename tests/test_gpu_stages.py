@@ -380,6 +380,36 @@ def test_elem_absmax_cast_bf16(ctx):
     assert np.array_equal(u32(wd), refw)
 
 
+def test_elem_absmax_cast_both_paths(ctx):
+    """Rows of whole float4s (n, astride, ao, bo multiples of 4, aligned
+    buffers) take the 16-byte kernels, others the per-element ones: both
+    against the oracle, bitwise for absmax and the cast."""
+    r = rng(29)
+    rows, n = 131, 768
+    a = (r.standard_normal((rows, 2 * n)) * 3).astype(np.float32)
+    for op, scale in [(0, 1.0), (1, 0.5)]:
+        ref = orc.qwen_elem(a, rows, n, 2 * n, 0, n, op, scale)
+        y = torch.empty(rows * n, dtype=torch.float32, device="cuda")
+        ctx.qwen_elem(rows, n, 2 * n, 0, n, op, scale, dev(a), y)
+        ctx.sync()
+        np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+    x = (r.standard_normal(100003) * 5).astype(np.float32)
+    x[77] = 1e4  # the maximum, in the scalar tail of neither path
+    for m in (100000, 100003, 99999):
+        xs = np.ascontiguousarray(x[:m])
+        amax0 = np.array([0, np.float32(1.0).view(np.uint32), 0], np.uint32)
+        ref_amax = orc.absmax(xs, amax0, 2)
+        amax = dev(amax0)
+        ctx.absmax(m, 2, dev(xs), amax)
+        ctx.sync()
+        assert np.array_equal(u32(amax), ref_amax), m
+        ref16 = orc.cast_f16(xs, ref_amax, 2)
+        dst = torch.empty(m, dtype=torch.float16, device="cuda")
+        ctx.cast_f16(m, 2, dev(xs), dst, dev(ref_amax))
+        ctx.sync()
+        assert np.array_equal(u16(dst), ref16), m
+
+
 def test_qwen_bf16_every_bit_pattern(ctx):
     """qwen_bf16 over all 65536 bf16 values in both halves of the word:
     overflow to inf, fp16 subnormals, values that flush to zero, both zeros,
