@@ -193,9 +193,27 @@ def measure_peaks(torch):
     torch.cuda.synchronize()
     tf = 2.0 * m ** 3 / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e12
     del a, b, c
+    # the vendor GEMM on the hot experts' shape of BASELINE config 4's
+    # gate_up: ten experts of 2048 rows, d 2048 -> 2I 1536, as one batched
+    # product on contiguous fp16 operands
+    nb, mr, kd, nn = 10, 2048, 2048, 1536
+    a = torch.randn(nb, mr, kd, dtype=torch.float16, device="cuda")
+    b = torch.randn(nb, kd, nn, dtype=torch.float16, device="cuda").contiguous()
+    for _ in range(2):
+        c = torch.bmm(a, b)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(10):
+        c = torch.bmm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    tf_hot = 2.0 * nb * mr * kd * nn / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e12
+    del a, b, c
     torch.cuda.empty_cache()
     return {"hbm_copy_GB/s": round(copy_gbs, 1), "hbm_copy": "1 GiB device copy, 2*bytes/t",
-            "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul"}
+            "fp16_gemm_TFLOP/s": round(tf, 1), "fp16_gemm": "8192^3 torch.matmul",
+            "fp16_gemm_hot_shape_TFLOP/s": round(tf_hot, 1),
+            "fp16_gemm_hot_shape": "torch.bmm 10 x (2048 x 2048) x (2048 x 1536), contiguous operands"}
 
 
 def measure_transient(step, torch, n=400, n_after=60, idle_s=2.0):
