@@ -240,14 +240,18 @@ def test_pack_bf16_input_equals_fp16_of_converted(ctx):
     assert rt[((k // 16) * cpad + c) * 16 + (k % 4) * 4 + (k % 16) // 4] == wr[c, k].item()
 
 
-def test_layer_nonfinite_tokens(ctx):
+@pytest.mark.parametrize("rows,experts", [(64, 16), (100, 64), (300, 64)],
+                         ids=["router_topk", "rank_topk", "route_kernel"])
+def test_layer_nonfinite_tokens(ctx, rows, experts):
     """A token whose activations are NaN has NaN logits, so no expert is
     selectable: its pairs carry RMDA_NONE through rank (not counted), the
     permutation (slot NONE), the work list and the combine (skipped), and its
     output row is 0 (no shared expert).  A token with one +inf activation has
     +inf or NaN logits.  Every other token's routing is bit-exact and its
-    output within tolerance."""
-    cfg = dict(name="nonfinite", rows=64, d=256, experts=16, topk=4, inter=128, shared=0, skew=False)
+    output within tolerance.  The three cases route in the router (16
+    columns), in the rank kernel (one rank block) and in route_kernel (two
+    rank blocks)."""
+    cfg = dict(name="nonfinite", rows=rows, d=256, experts=experts, topk=4, inter=128, shared=0, skew=False)
     inp = inputs.make_inputs(ctx, cfg, seed=13)
     inp["x"][5] = float("nan")
     inp["x"][9, 3] = float("inf")
@@ -255,13 +259,13 @@ def test_layer_nonfinite_tokens(ctx):
     ref = orc.layer(inputs.to_host(inp), tile=16)
     idx = u32(views["idx"])
     assert np.array_equal(idx, ref["idx"]), "expert indices (with RMDA_NONE)"
-    assert np.all(idx.reshape(64, 4)[5] == 0xFFFFFFFF), "a NaN token selects nothing"
+    assert np.all(idx.reshape(rows, 4)[5] == 0xFFFFFFFF), "a NaN token selects nothing"
     assert np.array_equal(u32(views["count"]), ref["count"]), "counts exclude unselected pairs"
     assert np.array_equal(u32(views["off"]), ref["off"])
     assert np.array_equal(u32(views["slot"]), ref["slot"])
     got = out.float().cpu().numpy()
     assert np.all(got[5] == 0.0), "no selected expert: zero output"
-    ok = np.ones(64, bool)
+    ok = np.ones(rows, bool)
     ok[[5, 9]] = False
     assert np.isfinite(got[ok]).all()
     max_abs, rel = out_metrics(got[ok], ref["out"][ok])
