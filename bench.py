@@ -76,6 +76,9 @@ def parse_args():
     ap.add_argument("--transient", action="store_true",
                     help="before the warm-up, time each of the first 400 layer calls of this fresh process, "
                          "then 60 more after a 2 s idle (the GPU's warm-up transient)")
+    ap.add_argument("--sustain", type=float, default=0.0, metavar="SECS",
+                    help="after the warm-up, run the layer back to back for SECS seconds with amd-smi sampling "
+                         "socket power and clocks, then profile the stages at that clock; prints that line only")
     return ap.parse_args()
 
 
@@ -241,6 +244,78 @@ def measure_transient(step, torch, n=400, n_after=60, idle_s=2.0):
             "block_mean_ms": [round(sum(b) / len(b), 4) for b in blocks],
             "block_min_ms": [round(min(b), 4) for b in blocks],
             "after_idle_ms": [round(x, 4) for x in after]}
+
+
+def smi_sample():
+    """Socket power (W) and clocks (MHz) of GPU 0 from amd-smi's text report
+    (`amd-smi metric -g 0 --power --clock`), or None where amd-smi is
+    missing or prints no power line."""
+    import subprocess
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-g", "0", "--power", "--clock"], capture_output=True, text=True,
+                           timeout=30)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    txt = r.stdout
+    pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", txt)
+    if pw is None:
+        return None
+    gfx = [float(v) for v in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([0-9.]+)\s*MHz", txt)]
+    mem = re.search(r"MEM_0:\s*\n\s*CLK:\s*([0-9.]+)\s*MHz", txt)
+    return {"socket_W": float(pw.group(1)), "gfx_MHz": gfx, "mem_MHz": float(mem.group(1)) if mem else None}
+
+
+def measure_sustained(step, ctx, torch, secs, prof_calls=200):
+    """The layer run back to back for `secs` seconds (batches of 200 calls,
+    one synchronisation each), with amd-smi sampled about once a second
+    after the first two seconds: sustained ms per call, socket power and the
+    GFX clock of each XCD (averaged over samples).  Then, still warm, the
+    stage profiler over `prof_calls` calls: each stage's time at the
+    sustained clock.  Shows whether a long run is held at the board's power
+    limit, and by how much that lowers the clock."""
+    import threading
+
+    samples = []
+    done = threading.Event()
+    t_start = time.perf_counter()
+
+    def sampler():
+        while not done.wait(1.0):
+            if time.perf_counter() - t_start >= 2.0:
+                s = smi_sample()
+                if s is not None:
+                    samples.append(s)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    n = 0
+    ctx.sync()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < secs:
+        for _ in range(200):
+            step()
+        ctx.sync()
+        n += 200
+    dt = time.perf_counter() - t0
+    done.set()
+    th.join()
+    ctx.prof_begin()
+    for _ in range(prof_calls):
+        step()
+    stage_ms, nc = ctx.prof_end()
+    event_us = 1000.0 * ctx.prof_empty_ms() / max(nc, 1)
+    res = {"seconds": round(dt, 2), "calls": n, "ms_per_call": round(1e3 * dt / n, 4),
+           "stage_us": {k: round(1e3 * v / max(nc, 1) - event_us, 2) for k, v in stage_ms.items() if v > 0},
+           "smi_samples": len(samples)}
+    if samples:
+        gfx = [sum(s["gfx_MHz"]) / len(s["gfx_MHz"]) for s in samples if s["gfx_MHz"]]
+        res["socket_W_mean"] = round(sum(s["socket_W"] for s in samples) / len(samples), 1)
+        res["socket_W_max"] = max(s["socket_W"] for s in samples)
+        if gfx:
+            res["gfx_MHz_mean"] = round(sum(gfx) / len(gfx), 1)
+            res["gfx_MHz_min_xcd"] = min(min(s["gfx_MHz"]) for s in samples if s["gfx_MHz"])
+        res["mem_MHz"] = samples[-1]["mem_MHz"]
+    return res
 
 
 def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
@@ -494,6 +569,14 @@ def main():
         step()
     ctx.sync()
     torch.cuda.synchronize()
+    if args.sustain > 0:
+        idle = smi_sample()
+        s = measure_sustained(step, ctx, torch, args.sustain)
+        s["idle_before"] = None if idle is None else {"socket_W": idle["socket_W"], "mem_MHz": idle["mem_MHz"]}
+        ctx.close()
+        print(json.dumps({"sustained": s, "config": {"workload": cfg["name"], "tokens": shape["rows"]}}),
+              flush=True)
+        return
 
     # timed region: K layer calls, bracketed by device synchronisation; events
     # between equal rounds of the K calls (no synchronisation inside) give the
