@@ -246,23 +246,28 @@ def measure_transient(step, torch, n=400, n_after=60, idle_s=2.0):
             "after_idle_ms": [round(x, 4) for x in after]}
 
 
-def smi_sample():
-    """Socket power (W) and clocks (MHz) of GPU 0 from amd-smi's text report
-    (`amd-smi metric -g 0 --power --clock`), or None where amd-smi is
-    missing or prints no power line."""
-    import subprocess
-    try:
-        r = subprocess.run(["amd-smi", "metric", "-g", "0", "--power", "--clock"], capture_output=True, text=True,
-                           timeout=30)
-    except (OSError, subprocess.TimeoutExpired):
-        return None
-    txt = r.stdout
+def parse_smi(txt):
+    """Socket power (W), the GFX clock of each XCD and the memory clock (MHz)
+    from the text of `amd-smi metric --power --clock`; None when the text
+    holds no socket power (amd-smi prints "N/A" where a sensor is missing)."""
     pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", txt)
     if pw is None:
         return None
     gfx = [float(v) for v in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([0-9.]+)\s*MHz", txt)]
     mem = re.search(r"MEM_0:\s*\n\s*CLK:\s*([0-9.]+)\s*MHz", txt)
     return {"socket_W": float(pw.group(1)), "gfx_MHz": gfx, "mem_MHz": float(mem.group(1)) if mem else None}
+
+
+def smi_sample():
+    """parse_smi of GPU 0's current report, or None where amd-smi is missing
+    or prints no power line."""
+    import subprocess
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-g", "0", "--power", "--clock"], capture_output=True, text=True,
+                           timeout=30)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    return parse_smi(r.stdout)
 
 
 def measure_sustained(step, ctx, torch, secs, prof_calls=200):
