@@ -115,6 +115,15 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     __shared__ uint32_t sh_slot[2];
     __shared__ uint32_t pre[RMDA_MAX_EXPERTS];   // count_all: pairs before this block
     __shared__ uint32_t post[RMDA_MAX_EXPERTS];  // count_all: pairs after it
+    // count_all counts pre and post into CS copies of each, lane l adding to
+    // copy l % CS, and then sums the copies.  A wave's lanes hold
+    // consecutive pairs, so under skewed routing (one expert in the same
+    // top-k slot of most tokens) half of a wave's lanes add to the same
+    // expert, and the LDS serialises adds to one word.  A row of CW words
+    // (one spare) puts copy s of expert e in its own bank.
+    constexpr uint32_t CS = NT >= 1024 ? 8u : 1u;  // count_all runs 1024-thread blocks
+    constexpr uint32_t CW = RMDA_MAX_EXPERTS + 1u;
+    __shared__ uint32_t hcopy[2 * CS * CW];  // [pre, post][CS][CW]
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = tid / RMDA_WAVE;
@@ -131,6 +140,11 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         run[e] = 0;
         pre[e] = 0;
         post[e] = 0;
+    }
+    if (all) {
+        for (uint32_t i = tid; i < 2 * CS * CW; i += NT) {
+            hcopy[i] = 0u;
+        }
     }
     // Top-k folded in: block r's wave w routes row 4r + w as route_kernel
     // does, storing its experts at device scope; the last block to finish
@@ -214,7 +228,7 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     auto count_add = [&](uint32_t i0) {
 #pragma unroll
         for (uint32_t u = 0; u < CB; u += 1) {
-            uint32_t *h = i0 + u * NT < own_lo ? pre : post;
+            uint32_t *h = hcopy + ((i0 + u * NT < own_lo ? 0u : CS) + lane % CS) * CW;
             const uint32_t q[4] = {cv[u].x, cv[u].y, cv[u].z, cv[u].w};
 #pragma unroll
             for (uint32_t t = 0; t < 4; t += 1) {
@@ -289,8 +303,20 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         if (b + 1 < nb && tid < a.npairs - 4 * n4) {
             const uint32_t e = a.idx[4 * n4 + tid];
             if (e < E) {
-                atomicAdd(&post[e], 1u);
+                atomicAdd(&hcopy[(CS + lane % CS) * CW + e], 1u);
             }
+        }
+        __syncthreads();
+        // thread i < E sums pre[i], thread E + i post[i]
+        for (uint32_t i = tid; i < 2 * E; i += NT) {
+            const uint32_t hi = i >= E ? 1u : 0u;
+            const uint32_t e = i - hi * E;
+            uint32_t n = 0;
+#pragma unroll
+            for (uint32_t c = 0; c < CS; c += 1) {
+                n += hcopy[(hi * CS + c) * CW + e];
+            }
+            (hi != 0 ? post : pre)[e] = n;
         }
         __syncthreads();
     } else if (nb > 1) {
@@ -550,10 +576,17 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
 template <bool VEC>
 __global__ __launch_bounds__(1024) void count_kernel(const uint32_t *__restrict__ idx, uint32_t npairs,
                                                      uint32_t experts, uint32_t *__restrict__ count) {
-    __shared__ uint32_t h[RMDA_MAX_EXPERTS];
+    // CS copies of the histogram, lane l adding to copy l % CS (rows of CW
+    // words, one spare so that the copies of one expert sit in different
+    // banks): under skewed routing many lanes of a wave hold the same expert,
+    // and the LDS serialises adds to one word
+    constexpr uint32_t CS = 8;
+    constexpr uint32_t CW = RMDA_MAX_EXPERTS + 1u;
+    __shared__ uint32_t hc[CS * CW];
     const uint32_t tid = threadIdx.x;
-    for (uint32_t e = tid; e < experts; e += 1024) {
-        h[e] = 0;
+    uint32_t *const h = hc + (tid % RMDA_WAVE % CS) * CW;
+    for (uint32_t i = tid; i < CS * CW; i += 1024) {
+        hc[i] = 0;
     }
     __syncthreads();
     uint32_t done = 0;
@@ -588,7 +621,12 @@ __global__ __launch_bounds__(1024) void count_kernel(const uint32_t *__restrict_
     }
     __syncthreads();
     for (uint32_t e = tid; e < experts; e += 1024) {
-        count[e] = h[e];
+        uint32_t n = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < CS; c += 1) {
+            n += hc[c * CW + e];
+        }
+        count[e] = n;
     }
 }
 

@@ -157,12 +157,17 @@ def test_route_bitexact(ctx, rows, experts, topk, stride):
     np.testing.assert_allclose(wt.cpu().numpy(), wt_r, rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("rows,experts,topk,shift", [
-    (9000, 128, 8, 0),   # 72 000 pairs: above the one-workgroup count, counted by the rank kernel
-    (5001, 64, 4, 1),    # idx one word past 16-byte alignment: the count kernel's scalar-load variant
+@pytest.mark.parametrize("rows,experts,topk,shift,hot", [
+    (9000, 128, 8, 0, 0),   # 72 000 pairs: above the one-workgroup count, counted by the rank kernel
+    (5001, 64, 4, 1, 0),    # idx one word past 16-byte alignment: the count kernel's scalar-load variant
+    # every token's top-k is mostly experts 0..7 (whole waves add to one counter), one-workgroup count
+    (2051, 128, 8, 0, 8),
+    (9001, 512, 10, 0, 6),  # the same above the one-workgroup count
 ])
-def test_route_counts_both_paths(ctx, rows, experts, topk, shift):
+def test_route_counts_both_paths(ctx, rows, experts, topk, shift, hot):
     p = planted_logits(rows, experts, experts, seed=rows)
+    if hot:
+        p[:, :hot] += 50.0  # finite rows of planted_logits stay finite; -inf and NaN columns stay unselectable
     idx_r, wt_r, cnt_r = orc.route(p, experts, topk)
     buf = empty_u32(rows * topk + shift)
     idx = buf[shift:]
