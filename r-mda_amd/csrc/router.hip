@@ -218,7 +218,7 @@ template <bool W_PACKED, bool FUSE, int TT, int TPW>
 __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     const uint16_t *__restrict__ x16, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t cpad, uint32_t stride,
-    uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, rmda_route_fuse_t fz) {
+    uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, rmda_route_fuse_t fz, uint32_t col0) {
     constexpr uint32_t NCOL = 16 * TPW;
     constexpr int KS = MF_KS;
     constexpr uint32_t NW = MF_NW;
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     const uint32_t L = d / NQ;
     const uint32_t nsub = L / KS;  // d % (8*KS) == 0 is a launch condition
     const uint32_t t0 = blockIdx.x * TOK;
-    const uint32_t c0 = blockIdx.y * NCOL;
+    const uint32_t c0 = col0 + blockIdx.y * NCOL;  // columns from col0 (the wide tile's remainder)
     const uint32_t kk = lane / 16;
     const uint32_t ln = lane % 16;  // A: token row; B: column within a tile
 
@@ -437,6 +437,199 @@ __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     }
 }
 
+// Wide tile for many tokens and many columns (T = 4096, 512 experts): the
+// same chunk chains, bit for bit, with the work cut the other way.  A
+// workgroup owns 64 tokens x 128 columns; each of its 8 waves owns 16 of the
+// columns for all 64 tokens and runs all 8 d-chunk chains of them, so the
+// eight partials of an output sit in one lane's registers and are added
+// there, left to right, with no LDS reduction.  The activations are staged
+// once per workgroup in LDS (fp32, double-buffered, one 16-k step of every
+// chunk at a time) and read by all eight waves; the weights come straight
+// from memory, each value used for four token tiles.  Against the 32 x 32
+// tile above this reads the activations 4x and the weights 2x less often
+// from L2 (config 5: 0.33 GB of L2-to-CU traffic instead of 0.81 GB) and keeps
+// the MFMAs fed from registers and LDS.
+//
+// Per 16-k step s the workgroup stages x[64 tokens][chunk q][16 k] for all 8
+// chunks into LDS as xs[buf][q][tt][lane] float4 (lane = 16*kk + i holds
+// token 16*tt + i, k = 16*(q*nsub + s) + 4*st + kk for st = 0..3, i.e. the A
+// operand of four consecutive MFMA steps), then each wave runs, per chunk,
+// four steps of v_mfma_f32_16x16x4f32 on its four token tiles.  The weight
+// float4 of chunk q for the next step is loaded as soon as this step's has
+// been used, a full step (8 chunks) ahead.
+constexpr uint32_t RW_TOK = 64;            // tokens per workgroup
+constexpr uint32_t RW_TT = RW_TOK / 16;    // token tiles per wave
+constexpr uint32_t RW_NW = 8;              // waves per workgroup
+constexpr uint32_t RW_COL = 16 * RW_NW;    // columns per workgroup
+constexpr uint32_t RW_NT = RW_NW * RMDA_WAVE;
+constexpr uint32_t RW_MIN_WGS = 192;       // use the wide tile when it gives at least this many workgroups
+
+__device__ __forceinline__ void rw_barrier() {
+    // LDS stores and reads of this wave done, then the workgroup barrier
+    // (no vmcnt wait: the weight loads of the next step stay in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__restrict__ x16,
+                                                            const float *__restrict__ w,
+                                                            const float *__restrict__ bias,
+                                                            float *__restrict__ proj, uint32_t rows, uint32_t d,
+                                                            uint32_t cols, uint32_t cpad, uint32_t stride,
+                                                            uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
+    __shared__ float4 xs[2][NQ][RW_TT][RMDA_WAVE];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % RMDA_WAVE;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
+    if (zero_words != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+        for (uint32_t i = tid; i < n_zero; i += RW_NT) {
+            zero_words[i] = 0;
+        }
+    }
+    const uint32_t L = d / NQ;
+    const uint32_t nsub = L / 16;  // d % 128 == 0 is a launch condition
+    const uint32_t t0 = blockIdx.x * RW_TOK;
+    const uint32_t kk = lane / 16;
+    const uint32_t c = blockIdx.y * RW_COL + wv * 16 + lane % 16;  // < cpad: the grid covers whole 128-column blocks
+    // weight float4 of chunk q, step s: steps 0..3 of lane (kk, column c)
+    const float *wc = w + ((size_t)c * 4 + kk) * 4;
+    const size_t wq = (size_t)nsub * cpad * 16;  // one chunk further
+    const size_t ws = (size_t)cpad * 16;         // one 16-k step further
+
+    // staging: thread tid takes the 8-element halves p = tid and tid + RW_NT
+    // of the step's 8 x 64 x 2 halves: chunk p / 128, token (p % 128) / 2,
+    // half p % 2 (k 8h .. 8h+7 of the step)
+    const uint16_t *xsrc[2];
+    uint32_t xdst[2];  // float index in xs[0] of the token's float4 for kk = 0, plus 2h
+#pragma unroll
+    for (uint32_t r = 0; r < 2; r += 1) {
+        const uint32_t pc = tid + r * RW_NT;
+        const uint32_t q = pc / 128;
+        const uint32_t tok = (pc % 128) / 2;
+        const uint32_t h = pc % 2;
+        const uint32_t row = t0 + tok < rows ? t0 + tok : rows - 1;  // rows past the matrix: never stored
+        xsrc[r] = x16 + (size_t)row * d + q * L + 8 * h;
+        xdst[r] = ((q * RW_TT + tok / 16) * RMDA_WAVE + tok % 16) * 4 + 2 * h;
+    }
+    float *const xsf = reinterpret_cast<float *>(&xs[0][0][0][0]);
+    constexpr uint32_t XBUF = NQ * RW_TT * RMDA_WAVE * 4;  // floats per buffer
+    uint4 xv[2];
+    auto load_x = [&](uint32_t s) {
+#pragma unroll
+        for (uint32_t r = 0; r < 2; r += 1) {
+            xv[r] = *reinterpret_cast<const uint4 *>(xsrc[r] + (size_t)s * 16);
+        }
+    };
+    // element o of a half is k offset 8h + o: kk = o % 4, step 2h + o / 4
+    auto store_x = [&](uint32_t buf) {
+#pragma unroll
+        for (uint32_t r = 0; r < 2; r += 1) {
+            const uint32_t u[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+#pragma unroll
+            for (uint32_t k4 = 0; k4 < 4; k4 += 1) {
+                // o = k4 and o = k4 + 4: words k4 / 2 and 2 + k4 / 2, half k4 % 2
+                const uint32_t lo = u[k4 / 2];
+                const uint32_t hi = u[2 + k4 / 2];
+                const float a = (k4 % 2) ? h_hi(lo) : h_lo(lo);
+                const float b = (k4 % 2) ? h_hi(hi) : h_lo(hi);
+                *reinterpret_cast<float2 *>(xsf + buf * XBUF + xdst[r] + k4 * 16 * 4) = make_float2(a, b);
+            }
+        }
+    };
+
+    rmda_f32x4 acc[RW_TT][NQ];
+#pragma unroll
+    for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; q += 1) {
+            acc[tt][q] = rmda_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // weights in two register sets that trade roles every step (a step
+    // multiplies with one and fills the other for the next step), so no
+    // register copies, and no wait for the loads in flight, sit at the loop's
+    // back edge
+    float4 wa[NQ], wn[NQ];
+#pragma unroll
+    for (uint32_t q = 0; q < NQ; q += 1) {
+        wa[q] = *reinterpret_cast<const float4 *>(wc + q * wq);
+    }
+    load_x(0);
+    store_x(0);
+    rw_barrier();
+    // Every step issues the same loads (the last one re-reads its own step,
+    // in bounds, and stores it to the idle buffer, never read), so the
+    // compiler's vmcnt waits count the weight loads a full step ahead.  The
+    // scheduling fences keep the issue order as written: the next step's
+    // activation loads first, then per chunk its fragment reads, MFMAs and
+    // the next step's weight load (left to itself the compiler sinks the
+    // loads to the end of the step and then waits for them there).
+    auto step = [&](uint32_t s, float4 (&wcur)[NQ], float4 (&wnext)[NQ]) __attribute__((always_inline)) {
+        const uint32_t buf = s % 2;
+        const uint32_t sn = s + 1 < nsub ? s + 1 : s;
+        load_x(sn);
+        __builtin_amdgcn_sched_barrier(0);
+        const float4 *xa = &xs[buf][0][0][lane];
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; q += 1) {
+            float4 a[RW_TT];
+#pragma unroll
+            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+                a[tt] = xa[(q * RW_TT + tt) * RMDA_WAVE];
+            }
+            const float4 bq = wcur[q];
+            wnext[q] = *reinterpret_cast<const float4 *>(wc + q * wq + (size_t)sn * ws);
+#pragma unroll
+            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+                acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].x, bq.x, acc[tt][q], 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+                acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].y, bq.y, acc[tt][q], 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+                acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].z, bq.z, acc[tt][q], 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+                acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].w, bq.w, acc[tt][q], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        store_x(1 - buf);  // the other buffer: every wave finished reading it before the last barrier
+        rw_barrier();
+    };
+    uint32_t s = 0;
+    for (; s + 1 < nsub; s += 2) {
+        step(s, wa, wn);
+        step(s + 1, wn, wa);
+    }
+    if (s < nsub) {
+        step(s, wa, wn);
+    }
+    // D[4*kk + v][lane % 16] of token tile tt is token 16*tt + 4*kk + v
+    const bool cok = c < cols;
+    const float bv = bias != nullptr && c < nbias ? bias[c] : 0.0f;
+#pragma unroll
+    for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v += 1) {
+            float sum = acc[tt][0][v];
+#pragma unroll
+            for (uint32_t q = 1; q < NQ; q += 1) {
+                sum = sum + acc[tt][q][v];
+            }
+            if (bias != nullptr && c < nbias) {
+                sum = sum + bv;
+            }
+            const uint32_t t = t0 + 16 * tt + 4 * kk + v;
+            if (t < rows && cok) {
+                proj[(size_t)t * stride + c] = sum;
+            }
+        }
+    }
+}
+
 // HF router weights [cols][d] -> packed [d/16][cpad][4][4]: element (k, c)
 // at ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4, zero columns past `cols`.
 // One thread per packed float; a one-time load-time reorder.
@@ -457,18 +650,19 @@ uint32_t rmda_router_cpad(uint32_t cols) { return (cols + RMDA_WAVE - 1) / RMDA_
 
 namespace {
 
+// columns [col0, cols) of the 32 x 32 (or 16 x 16) tile
 template <bool FUSE, int TT, int TPW>
 void launch_mf_tile(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
                     const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
-                    uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
-    const dim3 grid((rows + MF_TOK * TT - 1) / (MF_TOK * TT), FUSE ? 1 : (cols + 16 * TPW - 1) / (16 * TPW));
+                    uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz, uint32_t col0) {
+    const dim3 grid((rows + MF_TOK * TT - 1) / (MF_TOK * TT), FUSE ? 1 : (cols - col0 + 16 * TPW - 1) / (16 * TPW));
     const dim3 block(MF_NW * RMDA_WAVE);
     if (w_packed) {
         hipLaunchKernelGGL((router_mf_kernel<true, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
-                           cols, cpad, stride, nbias, zero_words, n_zero, fz);
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0);
     } else {
         hipLaunchKernelGGL((router_mf_kernel<false, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
-                           cols, cpad, stride, nbias, zero_words, n_zero, fz);
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0);
     }
 }
 
@@ -476,14 +670,35 @@ template <bool FUSE>
 void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
                const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
                uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
-    const uint32_t wgs = (rows + MF_TOK * MF_TT - 1) / (MF_TOK * MF_TT) * (FUSE ? 1u : (cols + MF_NCOL - 1) / MF_NCOL);
-    const bool small = wgs < MF_MIN_WGS && (!FUSE || cols <= 16u * MF_TPW_SMALL);
+    uint32_t col0 = 0;
+    if (!FUSE && w_packed) {
+        // the wide tile takes whole 128-column blocks when they give the GPU
+        // enough workgroups; the columns past them (the shared-expert gate)
+        // go to the tile below
+        const uint32_t nbw = cols / RW_COL;
+        if (nbw > 0 && (rows + RW_TOK - 1) / RW_TOK * nbw >= RW_MIN_WGS) {
+            const dim3 grid((rows + RW_TOK - 1) / RW_TOK, nbw);
+            hipLaunchKernelGGL(router_wide_kernel, grid, dim3(RW_NT), 0, s, x16, w, bias, proj, rows, d, cols, cpad,
+                               stride, nbias, zero_words, n_zero);
+            col0 = nbw * RW_COL;
+            zero_words = nullptr;
+            if (col0 == cols) {
+                return;
+            }
+        }
+    }
+    const uint32_t wgs = (rows + MF_TOK * MF_TT - 1) / (MF_TOK * MF_TT) *
+                         (FUSE ? 1u : (cols - col0 + MF_NCOL - 1) / MF_NCOL);
+    // a remainder of at most 16 columns (the shared gate) takes 16-column
+    // workgroups: a 32-column one would do twice the work for dead columns
+    const bool small = (wgs < MF_MIN_WGS || (col0 > 0 && cols - col0 <= 16u * MF_TPW_SMALL)) &&
+                       (!FUSE || cols <= 16u * MF_TPW_SMALL);
     if (small) {
         launch_mf_tile<FUSE, MF_TT_SMALL, MF_TPW_SMALL>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride,
-                                                        nbias, zero_words, n_zero, fz);
+                                                        nbias, zero_words, n_zero, fz, col0);
     } else {
         launch_mf_tile<FUSE, MF_TT, MF_TPW>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride, nbias,
-                                            zero_words, n_zero, fz);
+                                            zero_words, n_zero, fz, col0);
     }
 }
 

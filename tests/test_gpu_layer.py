@@ -106,6 +106,12 @@ TEACHER = dict(name="teacher", rows=256, d=2560, experts=512, topk=10, inter=640
     # 3081 pairs: several rank blocks that all count every pair (count_all), a
     # partial last block and npairs % 4 = 1 pairs past the 16-byte words
     dict(name="count_all_tail", rows=1027, d=256, experts=40, topk=3, inter=128, shared=0, skew=False),
+    # the wide router tile (64 tokens x 128 columns per workgroup, 49 x 4 of
+    # them, the last token block ragged), the shared gate's column 512 by the
+    # 32 x 32 tile in a second launch
+    dict(name="wide_router_shared", rows=3100, d=256, experts=512, topk=4, inter=128, shared=128, skew=False),
+    # 65 x 3 wide workgroups, no remainder columns, 6 k steps per router chunk
+    dict(name="wide_router_e384", rows=4100, d=768, experts=384, topk=6, inter=128, shared=0, skew=False),
     TEACHER,
 ], ids=lambda c: c["name"])
 def test_layer_more_shapes(ctx, cfg):
