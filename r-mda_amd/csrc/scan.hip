@@ -57,6 +57,45 @@ __device__ uint32_t block_exscan(uint32_t v, uint32_t *sbuf, uint32_t *total) {
     return base + x - v;
 }
 
+// block_exscan of v, and in the same pass (one pair of barriers) the block
+// totals of u1 and u2; sbuf holds 3 * NT / 64 words.
+template <uint32_t NT>
+__device__ uint32_t block_exscan3(uint32_t v, uint32_t u1, uint32_t u2, uint32_t *sbuf, uint32_t *total,
+                                  uint32_t *total1, uint32_t *total2) {
+    constexpr uint32_t NW = NT / RMDA_WAVE;
+    const uint32_t lane = threadIdx.x % RMDA_WAVE;
+    const uint32_t w = threadIdx.x / RMDA_WAVE;
+    uint32_t x[3] = {v, u1, u2};
+#pragma unroll
+    for (uint32_t j = 0; j < 3; j += 1) {
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x111, 0xF, 0xF, false);
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x112, 0xF, 0xF, false);
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x114, 0xF, 0xF, false);
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x118, 0xF, 0xF, false);
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x142, 0xA, 0xF, false);
+        x[j] += __builtin_amdgcn_update_dpp(0u, x[j], 0x143, 0xC, 0xF, false);
+    }
+    if (lane == RMDA_WAVE - 1) {
+        sbuf[w] = x[0];
+        sbuf[NW + w] = x[1];
+        sbuf[2 * NW + w] = x[2];
+    }
+    __syncthreads();
+    uint32_t base = 0;
+    uint32_t t[3] = {0u, 0u, 0u};
+    for (uint32_t i = 0; i < NW; i += 1) {
+        base += i < w ? sbuf[i] : 0u;
+        t[0] += sbuf[i];
+        t[1] += sbuf[NW + i];
+        t[2] += sbuf[2 * NW + i];
+    }
+    __syncthreads();
+    *total = t[0];
+    *total1 = t[1];
+    *total2 = t[2];
+    return base + x[0] - v;
+}
+
 // shader/moe_scan.comp:14-37, one thread per expert (experts <= 512).
 // tiles[t] is written once per t: the owner is found by binary search over
 // the inclusive padded prefix instead of relying on a pre-fill.
@@ -108,7 +147,7 @@ template <uint32_t NT, int NV>
 __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     __shared__ unsigned long long msk[NT / RMDA_WAVE][RMDA_MAX_EXPERTS];
     __shared__ uint32_t run[RMDA_MAX_EXPERTS];
-    __shared__ uint32_t sbuf[NT / RMDA_WAVE];
+    __shared__ uint32_t sbuf[3 * NT / RMDA_WAVE];  // block scans (block_exscan3 uses all three rows)
     __shared__ uint32_t s_last;
     __shared__ uint32_t cls_n[RMDA_ITEM_CLASSES];  // work-list items per 16-row class
     __shared__ uint32_t cls_b[RMDA_ITEM_CLASSES];
@@ -378,8 +417,14 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     }
     const uint32_t p0 = (c0 + a.tile - 1u) / a.tile * a.tile;
     const uint32_t p1 = (c1 + a.tile - 1u) / a.tile * a.tile;
+    // offsets, and with them the two totals the tile choice below needs
+    // (all rows; rows of experts with at least hot_min rows)
+    const uint32_t hm = a.hot_min;
     uint32_t total = 0;
-    const uint32_t base = block_exscan<NT>(p0 + p1, sbuf, &total);
+    uint32_t rows_all = 0;
+    uint32_t rows_hot = 0;
+    const uint32_t base = block_exscan3<NT>(p0 + p1, c0 + c1, (c0 >= hm ? c0 : 0u) + (c1 >= hm ? c1 : 0u), sbuf,
+                                            &total, &rows_all, &rows_hot);
     uint32_t o0 = base;
     uint32_t o1 = base + p0;
     if (a.off_in != nullptr) {
@@ -464,11 +509,6 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     uint32_t bm = a.bm;
     bool hot = false;
     if (a.n_items_hot != nullptr) {
-        const uint32_t hm = a.hot_min;
-        uint32_t rows_all = 0;
-        uint32_t rows_hot = 0;
-        block_exscan<NT>(c0 + c1, sbuf, &rows_all);
-        block_exscan<NT>((c0 >= hm ? c0 : 0u) + (c1 >= hm ? c1 : 0u), sbuf, &rows_hot);
         rows_all += a.shared_rows;
         rows_hot += a.shared_rows >= hm ? a.shared_rows : 0u;
         const bool hot_auto = hm > 0 && rows_hot > 0 && 2ull * rows_hot >= rows_all;
