@@ -132,7 +132,7 @@ def test_qwen_shim_scratch_sizing(L):
     n = L.rmda_qwen_moe_scratch_bytes(ctypes.byref(q))
     T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
     mrows = (T * K + E * 127 + 127) // 128 * 128
-    assert mrows == 32640  # SURVEY's config-3 figure (255 tiles)
+    assert mrows == 32640  # config 3: 2048 * 8 + 128 * 127 rounded up to 128 (255 tiles)
     # xp, g, hp, hp16 and ye alone
     assert n >= mrows * d * 2 + mrows * 2 * I * 4 + mrows * I * 6 + mrows * d * 4
     lay = _lib.QwenLayout()
