@@ -85,34 +85,26 @@ __device__ __forceinline__ float rmda_key_float(uint32_t k) {
     return __builtin_bit_cast(float, u);
 }
 
-template <int CTRL>
-__device__ __forceinline__ uint64_t rmda_dpp_u64(uint64_t v) {
-    const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)v, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ __forceinline__ uint64_t rmda_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-// Maximum over the wave, returned to every lane; the whole wave must be
-// active.  Register-only: DPP within each 16-lane row (swap neighbours, swap
-// pairs, mirror halves, mirror the row), then v_permlane16_swap and
-// v_permlane32_swap exchange rows and halves, so no step goes through the
-// LDS pipeline the way a generic lane shuffle (ds_bpermute) does.
-__device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
-    v = rmda_max_u64(v, rmda_dpp_u64<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = rmda_max_u64(v, rmda_dpp_u64<0x4E>(v));   // quad_perm [2,3,0,1]: quad max
-    v = rmda_max_u64(v, rmda_dpp_u64<0x141>(v));  // row_half_mirror: 8-lane max
-    v = rmda_max_u64(v, rmda_dpp_u64<0x140>(v));  // row_mirror: row max
+// Maximum (MAX) or minimum over the wave, returned to every lane; the whole
+// wave must be active.  Register-only: DPP within each 16-lane row (swap
+// neighbours, swap pairs, mirror halves, mirror the row), then
+// v_permlane16_swap and v_permlane32_swap exchange rows and halves, so no
+// step goes through the LDS pipeline the way a generic lane shuffle
+// (ds_bpermute) does.
+template <bool MAX>
+__device__ __forceinline__ uint32_t rmda_wave_red_u32(uint32_t v) {
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0u, v, 0x141, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0u, v, 0x140, 0xF, 0xF, false));
     {
-        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
-        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-        v = rmda_max_u64(((uint64_t)hi[0] << 32) | lo[0], ((uint64_t)hi[1] << 32) | lo[1]);  // 32-lane max
+        const auto x = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = op(x[0], x[1]);
     }
     {
-        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-        v = rmda_max_u64(((uint64_t)hi[0] << 32) | lo[0], ((uint64_t)hi[1] << 32) | lo[1]);  // wave max
+        const auto x = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = op(x[0], x[1]);
     }
     return v;
 }
@@ -125,8 +117,8 @@ __device__ __forceinline__ uint64_t rmda_wave_max_u64(uint64_t v) {
 // taken; idx in selection order; z = sum_k exp(l_k - l_0) summed in
 // selection order; wt_k = exp(l_k - l_0) / z; count[e] += 1 per selection
 // when count != NULL.  Lane l holds columns l, l+64, ...; a round is one
-// lane-local scan plus one wave-wide max over the 64-bit key
-// (order-preserving float bits << 32 | ~column).  AGENT: read the logits
+// lane-local scan, one wave-wide max of the order-preserving float key and
+// the lowest column among the lanes holding that maximum.  AGENT: read the logits
 // with device-scope loads (rows written by other workgroups of the running
 // kernel).
 template <int NV, bool AGENT>
@@ -169,16 +161,23 @@ __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t
                 lv = j;
             }
         }
-        uint64_t key = 0;
-        if (lv >= 0) {
-            key = ((uint64_t)rmda_float_key(lb) << 32) | (uint32_t)(~(lane + RMDA_WAVE * (uint32_t)lv));
-        }
-        key = rmda_wave_max_u64(key);
+        // the largest value over the wave (a selectable value's key is
+        // never 0), then the lowest column holding it: the column of the
+        // one lane holding it, or, on a tie across lanes, the least of the
+        // tied lanes' columns (each lane's scan already kept its lowest)
+        const uint32_t k32 = lv >= 0 ? rmda_float_key(lb) : 0u;
+        const uint32_t m32 = rmda_wave_red_u32<true>(k32);
         uint32_t col = RMDA_NONE;
         float val = -3.0e38f;
-        if (key != 0) {
-            col = ~(uint32_t)key;
-            val = rmda_key_float((uint32_t)(key >> 32));
+        if (m32 != 0) {
+            const uint32_t mine = lane + RMDA_WAVE * (uint32_t)lv;
+            const uint64_t tied = __ballot(k32 == m32);
+            if (__popcll(tied) == 1) {
+                col = __builtin_amdgcn_readlane(mine, (uint32_t)__ffsll((unsigned long long)tied) - 1u);
+            } else {
+                col = rmda_wave_red_u32<false>(k32 == m32 ? mine : 0xffffffffu);
+            }
+            val = rmda_key_float(m32);
             if (col % RMDA_WAVE == lane) {
                 taken |= 1u << (col / RMDA_WAVE);
             }

@@ -10,10 +10,11 @@
 // Here one wave owns one row (rmda_route_row in common.h).  Lane l holds
 // columns l, l+64, ... (coalesced; up to 8 per lane for 512 experts) instead
 // of the reference's 16 contiguous columns on 32 lanes.  A round is one
-// lane-local scan plus one wave-wide max over a 64-bit key (order-preserving
-// float bits << 32 | ~column), which yields the largest value and, among
-// equal values, the lowest column in a single reduction.  Only columns <
-// experts are read (the reference reads 512 columns regardless).
+// lane-local scan, one wave-wide max of the order-preserving float key,
+// which yields the largest value, and the lowest column holding it: read
+// from the one lane that holds the maximum or, when several lanes tie, a
+// wave-wide min over their columns.  Only columns < experts are read (the
+// reference reads 512 columns regardless).
 #include "common.h"
 
 namespace {
