@@ -306,7 +306,7 @@ struct rmda_rank_args_t {
     uint16_t *fc_zero_out;
     uint32_t fc_d;
     // top-k folded in (optional; npairs <= RMDA_RANK_BLOCK, done zero on
-    // entry): one block per 4 rows routes route_rows rows of logits
+    // entry): one block per 8 rows routes route_rows rows of logits
     // (route_proj, row stride route_stride) as route_kernel does, into
     // route_idx (which must be idx) and route_wt; the last of them ranks
     const float *route_proj;

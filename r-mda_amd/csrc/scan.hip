@@ -711,21 +711,25 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     // config 5, 20 blocks over 512 experts: rank 15.5 -> 10.2 us; config 3
     // 7.6 -> 7.35 us; one block is 0.15 us slower with 1024)
     if (a->route_proj != nullptr) {
-        // top-k folded in: one block per 4 rows routes, the last one ranks
+        // top-k folded in: one block per 8 rows routes, the last one ranks
+        // (8-wave blocks: decode rank 7.45-7.65 -> 7.16-7.19 us against 4-wave
+        // ones; 16-wave ones took 8.8-9.1, their last block then routing
+        // as well as ranking the most)
+        constexpr uint32_t NTR = 512;
         if (nb != 1 || a->experts > RMDA_MAX_EXPERTS || a->topk == 0 || a->done == nullptr ||
             a->route_rows * a->topk != a->npairs) {
             return hipErrorInvalidValue;
         }
         const uint32_t nv = (a->experts + RMDA_WAVE - 1) / RMDA_WAVE;
-        const dim3 g1((a->route_rows + NT0 / RMDA_WAVE - 1) / (NT0 / RMDA_WAVE)), b1(NT0);
+        const dim3 g1((a->route_rows + NTR / RMDA_WAVE - 1) / (NTR / RMDA_WAVE)), b1(NTR);
         if (nv <= 1) {
-            hipLaunchKernelGGL((rank_kernel<NT0, 1>), g1, b1, 0, s, *a);
+            hipLaunchKernelGGL((rank_kernel<NTR, 1>), g1, b1, 0, s, *a);
         } else if (nv <= 2) {
-            hipLaunchKernelGGL((rank_kernel<NT0, 2>), g1, b1, 0, s, *a);
+            hipLaunchKernelGGL((rank_kernel<NTR, 2>), g1, b1, 0, s, *a);
         } else if (nv <= 4) {
-            hipLaunchKernelGGL((rank_kernel<NT0, 4>), g1, b1, 0, s, *a);
+            hipLaunchKernelGGL((rank_kernel<NTR, 4>), g1, b1, 0, s, *a);
         } else {
-            hipLaunchKernelGGL((rank_kernel<NT0, RMDA_MAX_EXPERTS / RMDA_WAVE>), g1, b1, 0, s, *a);
+            hipLaunchKernelGGL((rank_kernel<NTR, RMDA_MAX_EXPERTS / RMDA_WAVE>), g1, b1, 0, s, *a);
         }
         return hipGetLastError();
     }
