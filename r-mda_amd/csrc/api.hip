@@ -683,8 +683,12 @@ int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc, const
                      "permute");
 }
 
-int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t *a, const uint16_t *b, float *c,
-                const uint32_t *amax, const uint32_t *tiles) {
+// rmda_moe_mm, and for the recording's own calls the same with the
+// segments' offsets and counts (live_off, live_count): rows past a segment's
+// routed rows are then not computed, and C keeps its old values there
+static int moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t *a, const uint16_t *b, float *c,
+                  const uint32_t *amax, const uint32_t *tiles, const uint32_t *live_off,
+                  const uint32_t *live_count) {
     int rc = enter(ctx);
     if (rc != RMDA_OK) {
         return rc;
@@ -717,9 +721,16 @@ int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t 
     g.sa = pc->sa;
     g.sb = pc->sb;
     if (rmda_ref_mm_supported(&g)) {
+        g.live_off = live_off;
+        g.live_count = live_count;
         return hip_check(ctx, rmda_launch_ref_mm(ctx->stream, &g, ctx->g2.grid), "moe_mm");
     }
-    return hip_check(ctx, rmda_launch_gemm(ctx->stream, &g), "moe_mm");
+    return hip_check(ctx, rmda_launch_gemm(ctx->stream, &g), "moe_mm");  // computes every row
+}
+
+int rmda_moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t *a, const uint16_t *b, float *c,
+                const uint32_t *amax, const uint32_t *tiles) {
+    return moe_mm(ctx, pc, a, b, c, amax, tiles, nullptr, nullptr);
 }
 
 static int combine_common(rmda_moe_ctx_t *ctx, const rmda_pc_moe_combine_t *pc, const float *wt,
@@ -1673,8 +1684,12 @@ int rmda_qwen_moe_layout(const rmda_qwen_moe_t *q, rmda_qwen_moe_layout_t *out) 
     return RMDA_OK;
 }
 
-int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out, uint32_t m,
-                     uint32_t n, uint32_t k) {
+namespace {
+
+// mda_qwen_moe_mm's work; live = true (the recording) leaves the padding
+// rows of each segment out of the GEMM, since nothing reads their results
+int qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out, uint32_t m,
+                uint32_t n, uint32_t k, bool live) {
     ShimPlan p;
     int rc = shim_enter(q, "rmda_qwen_moe_mm", &p);
     if (rc != RMDA_OK) {
@@ -1684,7 +1699,15 @@ int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const u
         return fail(q->ctx, RMDA_ERR_SHAPE, "rmda_qwen_moe_mm: m=%u beyond the scratch's %u rows", m, p.mrows);
     }
     const rmda_pc_moe_mm_t pc{m, n, k, sa, RMDA_NO_SLOT};
-    return rmda_moe_mm(q->ctx, &pc, a, w, out, scr<uint32_t>(q, p.amax), scr<uint32_t>(q, p.tiles));
+    return moe_mm(q->ctx, &pc, a, w, out, scr<uint32_t>(q, p.amax), scr<uint32_t>(q, p.tiles),
+                  live ? scr<uint32_t>(q, p.off) : nullptr, live ? scr<uint32_t>(q, p.count) : nullptr);
+}
+
+}  // namespace
+
+int rmda_qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out, uint32_t m,
+                     uint32_t n, uint32_t k) {
+    return qwen_moe_mm(q, a, sa, w, out, m, n, k, false);
 }
 
 namespace {
@@ -1787,14 +1810,17 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
                                           scr<float>(q, p.p), rows, d, p.ps, p.ps, 0, nullptr, 0, nullptr),
                        "moe_rec router");
     }
-    // A1-A3 (xp's padding rows are not zero-filled: the SwiGLU, absmax and
-    // cast below read the routed rows only)
+    // A1-A3 (xp's padding rows are not zero-filled: the GEMMs, SwiGLU,
+    // absmax and cast below compute the routed rows only)
     if (rc == RMDA_OK) {
         rc = route_rec(q, rows, mrows, false);
     }
-    // A4-A7: gate_up, SwiGLU, hp cast with a slot, down (src/qwen.c:847-878)
+    // A4-A7: gate_up, SwiGLU, hp cast with a slot, down (src/qwen.c:847-878).
+    // The reference's GEMMs also run every padding row of each 128-row
+    // segment (xp's zero rows, half of the rows at T=2048, E=128, top-8);
+    // their g and ye rows are never read, so these GEMMs skip them
     if (rc == RMDA_OK) {
-        rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d);
+        rc = qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d, true);
     }
     // SwiGLU and the absmax of hp in one pass (the same values and the same
     // slot value as qwen_elem then absmax), then the scaled cast
@@ -1803,9 +1829,10 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
         sh = shim_slot(q);
         rc = sh == RMDA_NO_SLOT ? c->err : RMDA_OK;
     }
-    // over the rows that hold routed pairs only: the padding rows of each
-    // 128-row segment are zero in g (xp's zero rows), so their SwiGLU is 0 and
-    // leaves the absmax unchanged, and nothing after reads their hp or ye
+    // over the rows that hold routed pairs only: in the reference the padding
+    // rows of each 128-row segment are zero in g (xp's zero rows), so their
+    // SwiGLU is 0 and leaves the absmax unchanged, and nothing after reads
+    // their hp or ye
     const rmda_rowmask_t live{scr<uint32_t>(q, p.tiles), scr<uint32_t>(q, p.off), scr<uint32_t>(q, p.count),
                               RMDA_QWEN_TILE};
     if (rc == RMDA_OK) {
@@ -1820,7 +1847,7 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
                        "moe_rec hp cast");
     }
     if (rc == RMDA_OK) {
-        rc = rmda_qwen_moe_mm(q, scr<uint16_t>(q, p.hp16), sh, q->w_down, scr<float>(q, p.ye), mrows, d, I);
+        rc = qwen_moe_mm(q, scr<uint16_t>(q, p.hp16), sh, q->w_down, scr<float>(q, p.ye), mrows, d, I, true);
     }
     // A8: the shared expert as one-expert grouped GEMMs over the padded rows
     // (src/qwen.c:879-886); rows past `rows` hold stale data and are unused

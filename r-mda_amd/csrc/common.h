@@ -395,6 +395,11 @@ struct rmda_gemm_args_t {
     const uint32_t *n_items;  // device word, or NULL: use max_items
     uint32_t max_items;       // grid bound
     const uint32_t *tiles;    // F32 mode: reference tile map instead of items
+    // F32 mode, optional (NULL: every row of a named tile): the segments'
+    // offsets and row counts; rows r of tile t at or past off[e] + count[e]
+    // (e = tiles[t]) are then neither computed nor stored
+    const uint32_t *live_off;
+    const uint32_t *live_count;
     const uint32_t *amax;
     uint32_t sa, sb;
     rmda_fc_t fc;             // F16 mode: the folded-in combine (fc.cnt == NULL: none)

@@ -20,7 +20,14 @@
 //   * 8 MFMA waves = 2 (M, 64 rows) x 4 (N, 64 columns),
 //     v_mfma_f32_16x16x32_f16, fp32 accumulate; they also write C.  Four more
 //     waves issue all of the DMA (4 A and 8 B instructions per stage each) and
-//     nothing else.  On gfx950 a wave's stores count in vmcnt like its loads,
+//     nothing else.
+//   * LIVE (the recording's own calls, rmda_gemm_args_t::live_count): a
+//     tile's rows past its segment's routed rows are padding whose results
+//     nothing reads, so 16-row groups wholly past them run no MFMAs (a wave
+//     whose 64 rows are all padding reads no fragments either), their rows
+//     are not stored, and their A loads read the tile's first row again
+//     instead of HBM.  At config 3 a third of the used tiles' rows are
+//     padding.  On gfx950 a wave's stores count in vmcnt like its loads,
 //     so a wave that both streamed the stages and wrote a finished tile's
 //     128 KiB of fp32 C would drain its whole load pipeline at every wait
 //     after a tile; measured at BASELINE config 3, the stores then cost
@@ -55,6 +62,7 @@ __device__ __forceinline__ float ref_slot_scale(const uint32_t *amax, uint32_t s
     return ldexpf(1.0f, 141 - (int)((u >> 23) & 0xffu));
 }
 
+template <bool LIVE>
 __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t CH = RK / 8;                 // 16-byte chunks per row
     constexpr uint32_t RPI = 64 / CH;               // rows per DMA instruction
@@ -68,6 +76,7 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     static_assert(2 * L_PER < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[RSTAGES * STAGE_BYTES];
     __shared__ uint16_t tl[MAX_TILES];
+    __shared__ uint8_t tlive[LIVE ? MAX_TILES : 1];  // LIVE: rows of the compacted tile to compute, 0..RM
     __shared__ uint32_t nv_w[RMW + RIW];
 
     const uint32_t tid = threadIdx.x;
@@ -94,7 +103,17 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         }
         if (ok) {
             const uint64_t below = lane == 0 ? 0ull : (~0ull >> (RMDA_WAVE - lane));
-            tl[before + (uint32_t)__popcll(m & below)] = (uint16_t)t;
+            const uint32_t ci = before + (uint32_t)__popcll(m & below);
+            tl[ci] = (uint16_t)t;
+            if constexpr (LIVE) {
+                // rows [t*RM, off + count) of the segment; a map whose segment
+                // starts past the tile keeps the whole tile
+                const uint32_t e = g.tiles[t];
+                const uint64_t lo = (uint64_t)t * RM;
+                const uint64_t off = g.live_off[e];
+                const uint64_t end = off + g.live_count[e];
+                tlive[ci] = (uint8_t)(off > lo ? RM : end <= lo ? 0u : (uint32_t)min(end - lo, (uint64_t)RM));
+            }
         }
         n_valid += all;
         __syncthreads();
@@ -117,13 +136,18 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         const uint16_t *b_src[B_PER];
         auto setup = [&](uint32_t q) __attribute__((always_inline)) {
             uint32_t nt;
-            const uint32_t t = tl[sched.item(q, nt)];
+            const uint32_t ci = sched.item(q, nt);
+            const uint32_t t = tl[ci];
             const uint32_t grp = g.tiles[t];
             const uint16_t *wg = g.w + (size_t)grp * g.n_w * g.k;
+            // LIVE: padding rows load the tile's first row instead (a cache
+            // hit, not an HBM read); their results are not stored
+            const uint32_t lv = LIVE ? (uint32_t)tlive[ci] : RM;
 #pragma unroll
             for (uint32_t j = 0; j < A_PER; j += 1) {
                 const uint32_t r = (dw * A_PER + j) * RPI + lrow;
-                a_src[j] = g.a + (size_t)(t * RM + r) * g.lda + (lch ^ swz<RK>(r)) * 8;
+                const uint32_t ra = r < lv ? r : 0u;
+                a_src[j] = g.a + (size_t)(t * RM + ra) * g.lda + (lch ^ swz<RK>(r)) * 8;
             }
 #pragma unroll
             for (uint32_t j = 0; j < B_PER; j += 1) {
@@ -192,17 +216,26 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     uint32_t kc = 0;
     uint32_t ks = 0;
     uint32_t cbuf = 0;
+    uint32_t lrows = RM;  // LIVE: rows of the current task's tile to compute and store
+    uint32_t ngrp = 4;    // LIVE: 16-row groups of this wave's 64 rows that hold such rows
     for (uint32_t gs = 0; gs < nstage; gs += 1) {
         lds_barrier();
+        if (LIVE && ks == 0) {
+            uint32_t nt;
+            lrows = __builtin_amdgcn_readfirstlane(tlive[sched.item(kc, nt)]);
+            ngrp = lrows > wm * 64 ? min(4u, (lrows - wm * 64 + 15) / 16) : 0u;
+        }
         const uint8_t *base = smem + cbuf * STAGE_BYTES;
         cbuf = cbuf + 1 == RSTAGES ? 0 : cbuf + 1;
         half8_t fa[2][4], fb[2][4];
+        if (!LIVE || ngrp > 0) {
 #pragma unroll
-        for (int i = 0; i < 4; i += 1) {
-            fa[0][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c0);
-            fb[0][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c0);
-            fa[1][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c1);
-            fb[1][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c1);
+            for (int i = 0; i < 4; i += 1) {
+                fa[0][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c0);
+                fb[0][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c0);
+                fa[1][i] = *reinterpret_cast<const half8_t *>(base + a_row + i * 16 * (RK * 2) + c1);
+                fb[1][i] = *reinterpret_cast<const half8_t *>(base + b_row + i * 16 * (RK * 2) + c1);
+            }
         }
         lds_barrier();  // the stage is in registers: the issue waves may refill its buffer
         if (ks == 0) {
@@ -218,9 +251,11 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         for (uint32_t kk = 0; kk < 2; kk += 1) {
 #pragma unroll
             for (int i = 0; i < 4; i += 1) {
+                if (!LIVE || (uint32_t)i < ngrp) {
 #pragma unroll
-                for (int j = 0; j < 4; j += 1) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < 4; j += 1) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -230,9 +265,16 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
             const uint32_t t = tl[sched.item(kc, nt)];
 #pragma unroll
             for (int i = 0; i < 4; i += 1) {
+                if (LIVE && (uint32_t)i >= ngrp) {
+                    continue;
+                }
 #pragma unroll
                 for (int v = 0; v < 4; v += 1) {
-                    const size_t r = (size_t)t * RM + wm * 64 + i * 16 + rq + v;
+                    const uint32_t rt = wm * 64 + i * 16 + rq + v;  // row within the tile
+                    if (LIVE && rt >= lrows) {
+                        continue;
+                    }
+                    const size_t r = (size_t)t * RM + rt;
 #pragma unroll
                     for (int j = 0; j < 4; j += 1) {
                         __builtin_nontemporal_store(acc[i][j][v] * sc, &C[r * g.ldo + nt * RN + wn * 64 + j * 16 + fr]);
@@ -262,6 +304,13 @@ hipError_t rmda_launch_ref_mm(hipStream_t s, const rmda_gemm_args_t *a, uint32_t
         return hipSuccess;
     }
     const dim3 gr(grid >= 8 ? grid / 8 * 8 : 8);
-    hipLaunchKernelGGL(ref_mm_kernel, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+    if (a->live_count != nullptr) {
+        if (a->live_off == nullptr) {
+            return hipErrorInvalidValue;
+        }
+        hipLaunchKernelGGL(ref_mm_kernel<true>, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+    } else {
+        hipLaunchKernelGGL(ref_mm_kernel<false>, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+    }
     return hipGetLastError();
 }
