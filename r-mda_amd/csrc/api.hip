@@ -685,10 +685,21 @@ int rmda_moe_scatter(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scatter_t *pc, const
 
 // rmda_moe_mm, and for the recording's own calls the same with the
 // segments' offsets and counts (live_off, live_count): rows past a segment's
-// routed rows are then not computed, and C keeps its old values there
+// routed rows are then not computed, and C keeps its old values there.
+// With swi (the recording's gate_up; a shape the persistent kernel takes)
+// the kernel writes SwiGLU(C) to swi->out and its absmax to amax[swi->so]
+// instead of C, and *swi->fused says whether it did.
+struct mm_swiglu_t {
+    float *out;
+    uint32_t so;
+    bool fused;
+};
 static int moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_t *a, const uint16_t *b, float *c,
                   const uint32_t *amax, const uint32_t *tiles, const uint32_t *live_off,
-                  const uint32_t *live_count) {
+                  const uint32_t *live_count, mm_swiglu_t *swi = nullptr) {
+    if (swi != nullptr) {
+        swi->fused = false;
+    }
     int rc = enter(ctx);
     if (rc != RMDA_OK) {
         return rc;
@@ -723,6 +734,13 @@ static int moe_mm(rmda_moe_ctx_t *ctx, const rmda_pc_moe_mm_t *pc, const uint16_
     if (rmda_ref_mm_supported(&g)) {
         g.live_off = live_off;
         g.live_count = live_count;
+        if (swi != nullptr && swi->out != nullptr) {
+            g.f32_swiglu = 1;
+            g.so = swi->so;
+            g.out = swi->out;
+            g.ldo = pc->n / 2;
+            swi->fused = true;
+        }
         return hip_check(ctx, rmda_launch_ref_mm(ctx->stream, &g, ctx->g2.grid), "moe_mm");
     }
     return hip_check(ctx, rmda_launch_gemm(ctx->stream, &g), "moe_mm");  // computes every row
@@ -1679,6 +1697,8 @@ int rmda_qwen_moe_layout(const rmda_qwen_moe_t *q, rmda_qwen_moe_layout_t *out) 
     out->slot = p.slot;
     out->xp = p.xp;
     out->amax = p.amax;
+    out->hp = p.hp;
+    out->tiles = p.tiles;
     out->total = p.total;
     out->p_stride = p.ps;
     return RMDA_OK;
@@ -1689,7 +1709,7 @@ namespace {
 // mda_qwen_moe_mm's work; live = true (the recording) leaves the padding
 // rows of each segment out of the GEMM, since nothing reads their results
 int qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16_t *w, float *out, uint32_t m,
-                uint32_t n, uint32_t k, bool live) {
+                uint32_t n, uint32_t k, bool live, mm_swiglu_t *swi = nullptr) {
     ShimPlan p;
     int rc = shim_enter(q, "rmda_qwen_moe_mm", &p);
     if (rc != RMDA_OK) {
@@ -1700,7 +1720,7 @@ int qwen_moe_mm(rmda_qwen_moe_t *q, const uint16_t *a, uint32_t sa, const uint16
     }
     const rmda_pc_moe_mm_t pc{m, n, k, sa, RMDA_NO_SLOT};
     return moe_mm(q->ctx, &pc, a, w, out, scr<uint32_t>(q, p.amax), scr<uint32_t>(q, p.tiles),
-                  live ? scr<uint32_t>(q, p.off) : nullptr, live ? scr<uint32_t>(q, p.count) : nullptr);
+                  live ? scr<uint32_t>(q, p.off) : nullptr, live ? scr<uint32_t>(q, p.count) : nullptr, swi);
 }
 
 }  // namespace
@@ -1817,17 +1837,21 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
     }
     // A4-A7: gate_up, SwiGLU, hp cast with a slot, down (src/qwen.c:847-878).
     // The reference's GEMMs also run every padding row of each 128-row
-    // segment (xp's zero rows, half of the rows at T=2048, E=128, top-8);
-    // their g and ye rows are never read, so these GEMMs skip them
-    if (rc == RMDA_OK) {
-        rc = qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d, true);
-    }
-    // SwiGLU and the absmax of hp in one pass (the same values and the same
-    // slot value as qwen_elem then absmax), then the scaled cast
+    // segment (xp's zero rows, a third of the used rows at T=2048, E=128,
+    // top-8); their g and ye rows are never read, so these GEMMs skip them.
+    // gate_up writes SwiGLU(g) and its absmax (hp's scale slot) from its
+    // epilogue, the same values as qwen_elem then absmax on g, so g itself
+    // never goes to memory (where the persistent kernel does not take the
+    // shape, g is written and the pass below computes them)
     uint32_t sh = RMDA_NO_SLOT;
     if (rc == RMDA_OK) {
-        sh = shim_slot(q);
+        sh = shim_slot(q);  // the slot qwen.c takes after gate_up: the same index
         rc = sh == RMDA_NO_SLOT ? c->err : RMDA_OK;
+    }
+    mm_swiglu_t swi{scr<float>(q, p.hp), sh, false};
+    if (rc == RMDA_OK) {
+        rc = qwen_moe_mm(q, scr<uint16_t>(q, p.xp), sx, q->w_gate_up, scr<float>(q, p.g), mrows, 2 * I, d, true,
+                         &swi);
     }
     // over the rows that hold routed pairs only: in the reference the padding
     // rows of each 128-row segment are zero in g (xp's zero rows), so their
@@ -1835,7 +1859,7 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
     // their hp or ye
     const rmda_rowmask_t live{scr<uint32_t>(q, p.tiles), scr<uint32_t>(q, p.off), scr<uint32_t>(q, p.count),
                               RMDA_QWEN_TILE};
-    if (rc == RMDA_OK) {
+    if (rc == RMDA_OK && !swi.fused) {
         const rmda_pc_qwen_elem_t pe{mrows, I, 2 * I, 0, I, 0, 1.0f};
         rc = hip_check(c, rmda_launch_elem_absmax_rows(c->stream, &pe, scr<float>(q, p.g), scr<float>(q, p.hp), amax,
                                                        sh, &live),

@@ -13,6 +13,12 @@
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
+// qwen_elem op 0 (shader/qwen_elem.comp:20-31): silu(g) * u, one expression
+// for every kernel that computes it, so they agree bit for bit
+__device__ __forceinline__ float rmda_swiglu(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
 __device__ __forceinline__ float rmda_h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
@@ -400,6 +406,12 @@ struct rmda_gemm_args_t {
     // (e = tiles[t]) are then neither computed nor stored
     const uint32_t *live_off;
     const uint32_t *live_count;
+    // F32 mode, optional: out is silu(C[:, j]) * C[:, n_w/2 + j] (qwen_elem
+    // op 0 on C) as [m][n_w/2] fp32, and amax[so] takes the absmax of what is
+    // stored (atomicMax of the bits, as rmda_launch_elem_absmax); needs the
+    // persistent kernel (rmda_ref_mm_supported) and n_w % 256 == 0
+    int f32_swiglu;
+    uint32_t so;
     const uint32_t *amax;
     uint32_t sa, sb;
     rmda_fc_t fc;             // F16 mode: the folded-in combine (fc.cnt == NULL: none)

@@ -19,7 +19,7 @@ __global__ __launch_bounds__(256) void elem_kernel(rmda_pc_qwen_elem_t pc, const
     const uint32_t c = (uint32_t)(i % pc.n);
     const float g = a[(size_t)r * pc.astride + pc.ao + c];
     if (pc.op == 0) {
-        y[i] = g / (1.0f + expf(-g)) * a[(size_t)r * pc.astride + pc.bo + c];
+        y[i] = rmda_swiglu(g, a[(size_t)r * pc.astride + pc.bo + c]);
     } else {
         const float v = g * pc.scale;
         y[i] = v / (1.0f + expf(-v));
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void elem_absmax_kernel(rmda_pc_qwen_elem_t pc
         const uint32_t r = (uint32_t)(i / pc.n);
         const uint32_t c = (uint32_t)(i % pc.n);
         const float g = a[(size_t)r * pc.astride + pc.ao + c];
-        const float v = g / (1.0f + expf(-g)) * a[(size_t)r * pc.astride + pc.bo + c];
+        const float v = rmda_swiglu(g, a[(size_t)r * pc.astride + pc.bo + c]);
         y[i] = v;
         m = fmaxf(m, fabsf(v));
     }
@@ -108,10 +108,6 @@ __global__ __launch_bounds__(256) void cast_kernel(const float *__restrict__ src
 // per lane, a block per (column range, row stride) so no index needs a
 // division.  The absmax kernels reduce per block and merge with one
 // atomicMax per block (at most 1024 blocks).
-__device__ __forceinline__ float swiglu1(float g, float u) {
-    return g / (1.0f + expf(-g)) * u;
-}
-
 __device__ __forceinline__ float silu_scaled1(float g, float scale) {
     const float v = g * scale;
     return v / (1.0f + expf(-v));
@@ -156,7 +152,8 @@ __global__ __launch_bounds__(256) void elem4_kernel(rmda_pc_qwen_elem_t pc, cons
             float4 v;
             if (pc.op == 0) {
                 const float4 u = ua[c];
-                v = make_float4(swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w));
+                v = make_float4(rmda_swiglu(g.x, u.x), rmda_swiglu(g.y, u.y), rmda_swiglu(g.z, u.z),
+                                rmda_swiglu(g.w, u.w));
             } else {
                 v = make_float4(silu_scaled1(g.x, pc.scale), silu_scaled1(g.y, pc.scale),
                                 silu_scaled1(g.z, pc.scale), silu_scaled1(g.w, pc.scale));

@@ -27,7 +27,13 @@
 //     whose 64 rows are all padding reads no fragments either), their rows
 //     are not stored, and their A loads read the tile's first row again
 //     instead of HBM.  At config 3 a third of the used tiles' rows are
-//     padding.  On gfx950 a wave's stores count in vmcnt like its loads,
+//     padding.
+//   * SWI (rmda_gemm_args_t::f32_swiglu, the recording's gate_up): the N
+//     tile is 128 gate columns j and their 128 up columns n_w/2 + j, laid out
+//     so that each MFMA wave holds 32 of each for the same 32 outputs (LDS
+//     rows 64w .. 64w+31 gate, 64w+32 .. 64w+63 up); the epilogue writes
+//     silu(g) * u in place of the two fp32 columns and folds the absmax
+//     that the next cast needs, so C never goes to memory.  On gfx950 a wave's stores count in vmcnt like its loads,
 //     so a wave that both streamed the stages and wrote a finished tile's
 //     128 KiB of fp32 C would drain its whole load pipeline at every wait
 //     after a tile; measured at BASELINE config 3, the stores then cost
@@ -62,7 +68,7 @@ __device__ __forceinline__ float ref_slot_scale(const uint32_t *amax, uint32_t s
     return ldexpf(1.0f, 141 - (int)((u >> 23) & 0xffu));
 }
 
-template <bool LIVE>
+template <bool LIVE, bool SWI>
 __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t CH = RK / 8;                 // 16-byte chunks per row
     constexpr uint32_t RPI = 64 / CH;               // rows per DMA instruction
@@ -151,8 +157,12 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
             }
 #pragma unroll
             for (uint32_t j = 0; j < B_PER; j += 1) {
-                const uint32_t n = (dw * B_PER + j) * RPI + lrow;
-                b_src[j] = wg + (size_t)(nt * RN + n) * g.k + (lch ^ swz<RK>(n)) * 8;
+                const uint32_t n = (dw * B_PER + j) * RPI + lrow;  // LDS row
+                // SWI: LDS rows 64w + c (c < 32) hold gate column 128 nt + 32w + c,
+                // 64w + 32 + c the matching up column n_w / 2 + 128 nt + 32w + c
+                const uint32_t wr = SWI ? (n % 64 < 32 ? 0u : g.n_w / 2) + nt * (RN / 2) + (n / 64) * 32 + n % 32
+                                        : nt * RN + n;
+                b_src[j] = wg + (size_t)wr * g.k + (lch ^ swz<RK>(n)) * 8;
             }
         };
         uint32_t i_task = 0;
@@ -213,6 +223,7 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     const float sc = 1.0f / (ref_slot_scale(g.amax, g.sa) * ref_slot_scale(g.amax, g.sb));
     float *C = reinterpret_cast<float *>(g.out);
     floatx4_t acc[4][4];
+    float amx = 0.0f;  // SWI: absmax of the stored outputs
     uint32_t kc = 0;
     uint32_t ks = 0;
     uint32_t cbuf = 0;
@@ -275,9 +286,20 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
                         continue;
                     }
                     const size_t r = (size_t)t * RM + rt;
+                    if constexpr (SWI) {
+                        // columns j (gate) and j + 2 (up) of this wave are the same outputs
 #pragma unroll
-                    for (int j = 0; j < 4; j += 1) {
-                        __builtin_nontemporal_store(acc[i][j][v] * sc, &C[r * g.ldo + nt * RN + wn * 64 + j * 16 + fr]);
+                        for (int j = 0; j < 2; j += 1) {
+                            const float h = rmda_swiglu(acc[i][j][v] * sc, acc[i][j + 2][v] * sc);
+                            amx = fmaxf(amx, fabsf(h));
+                            __builtin_nontemporal_store(h, &C[r * g.ldo + nt * (RN / 2) + wn * 32 + j * 16 + fr]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j += 1) {
+                            __builtin_nontemporal_store(acc[i][j][v] * sc,
+                                                        &C[r * g.ldo + nt * RN + wn * 64 + j * 16 + fr]);
+                        }
                     }
                 }
             }
@@ -286,6 +308,17 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         if (ks == steps) {
             ks = 0;
             kc += 1;
+        }
+    }
+    if constexpr (SWI) {
+        // the same fmaxf of fabsf as the absmax kernels, over the wave, then
+        // one atomicMax of the bits per wave (all values non-negative)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            amx = fmaxf(amx, __shfl_xor(amx, o));
+        }
+        if (lane == 0 && g.so != RMDA_NO_SLOT) {
+            atomicMax(const_cast<uint32_t *>(&g.amax[g.so]), __builtin_bit_cast(uint32_t, amx));
         }
     }
 }
@@ -304,13 +337,21 @@ hipError_t rmda_launch_ref_mm(hipStream_t s, const rmda_gemm_args_t *a, uint32_t
         return hipSuccess;
     }
     const dim3 gr(grid >= 8 ? grid / 8 * 8 : 8);
-    if (a->live_count != nullptr) {
-        if (a->live_off == nullptr) {
-            return hipErrorInvalidValue;
+    const dim3 bl((RMW + RIW) * RMDA_WAVE);
+    if ((a->live_count != nullptr) != (a->live_off != nullptr) ||
+        (a->f32_swiglu && (a->amax == nullptr && a->so != RMDA_NO_SLOT))) {
+        return hipErrorInvalidValue;
+    }
+    if (a->f32_swiglu) {
+        if (a->live_count != nullptr) {
+            hipLaunchKernelGGL((ref_mm_kernel<true, true>), gr, bl, 0, s, *a);
+        } else {
+            hipLaunchKernelGGL((ref_mm_kernel<false, true>), gr, bl, 0, s, *a);
         }
-        hipLaunchKernelGGL(ref_mm_kernel<true>, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+    } else if (a->live_count != nullptr) {
+        hipLaunchKernelGGL((ref_mm_kernel<true, false>), gr, bl, 0, s, *a);
     } else {
-        hipLaunchKernelGGL(ref_mm_kernel<false>, gr, dim3((RMW + RIW) * RMDA_WAVE), 0, s, *a);
+        hipLaunchKernelGGL((ref_mm_kernel<false, false>), gr, bl, 0, s, *a);
     }
     return hipGetLastError();
 }

@@ -330,6 +330,7 @@ class QwenMoe:
         """Typed views of the chunk's routing intermediates in the scratch."""
         lay, q = self.layout, self.q
         K, E = q.topk, q.experts
+        mrows = (rows * K + E * 127 + 127) // 128 * 128  # mda_qwen_moe_rows (src/qwen.c:68-70)
 
         def view(off, n, dtype):
             nbytes = n * torch.tensor([], dtype=dtype).element_size()
@@ -342,4 +343,7 @@ class QwenMoe:
             "count": view(lay["count"], E, torch.int32),
             "off": view(lay["off"], E, torch.int32),
             "slot": view(lay["slot"], rows * K, torch.int32),
+            "amax": view(lay["amax"], 16, torch.int32),
+            "hp": view(lay["hp"], mrows * q.inter, torch.float32).view(mrows, q.inter),
+            "tiles": view(lay["tiles"], mrows // 128, torch.int32),
         }

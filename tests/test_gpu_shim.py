@@ -97,6 +97,49 @@ def test_moe_rec_hyper_connection_streams(ctx, cfg, hc, stride, rank):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
+FUSED_SWIGLU = [configs.CONFIGS[2], configs.CONFIGS[3], SHAPES[3], SHAPES[4]]
+
+
+@pytest.mark.parametrize("cfg", FUSED_SWIGLU, ids=[c["name"] for c in FUSED_SWIGLU])
+def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
+    """The recording's gate_up writes SwiGLU(g) and hp's absmax slot from its
+    epilogue and skips the padding rows of each 128-row segment.  On every row
+    that holds a routed pair, hp must be bitwise the public drop-ins run as
+    the reference runs them (rmda_moe_mm over the whole tiles, fp32 g, then
+    rmda_qwen_elem op 0), and the slot the absmax of those rows."""
+    print("fused swiglu %s" % cfg["name"], flush=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=5)
+    T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
+    q = make_shim(ctx, inp)
+    q.scratch.fill_(255)
+    out = torch.empty(T, d, dtype=torch.float16, device="cuda")
+    q.moe_rec(inp["x"].float(), T, out=out)
+    ctx.sync()
+    v = q.views(T)
+    mrows = v["hp"].shape[0]
+    off, count = u32(v["off"]), u32(v["count"])
+    live = np.zeros(mrows, dtype=bool)
+    for e in range(E):
+        live[off[e]:off[e] + count[e]] = True
+    assert live.sum() == T * K
+    hp = v["hp"].cpu().numpy()[live]
+    slots = v["amax"].clone()
+    # the reference's sequence on the same xp and x slot (slot 0)
+    lay = q.layout
+    xp = q.scratch[lay["xp"]:lay["xp"] + mrows * d * 2].view(torch.float16).view(mrows, d)
+    g32 = torch.empty(mrows, 2 * I, dtype=torch.float32, device="cuda")
+    ctx.mm(mrows, 2 * I, d, 0, 0xFFFFFFFF, xp, inp["w_gate_up"], g32, slots, v["tiles"])
+    hp_ref = torch.empty(mrows, I, dtype=torch.float32, device="cuda")
+    ctx.qwen_elem(mrows, I, 2 * I, 0, I, 0, 1.0, g32, hp_ref)
+    ctx.sync()
+    ref = hp_ref.cpu().numpy()[live]
+    assert np.isfinite(ref).all()
+    bad = np.flatnonzero((hp.view(np.uint32) != ref.view(np.uint32)).any(axis=1))
+    assert bad.size == 0, "rows differ: %s" % bad[:8]
+    amax = np.float32(np.abs(ref).max())
+    assert slots[1].item() == int(amax.view(np.int32)), (slots[1].item(), amax)
+
+
 def test_moe_rec_runs_twice_bitwise_and_chunks(ctx):
     """Run-to-run determinism, and a smaller second chunk through the same
     scratch (laid out for max_rows) gives the oracle's answer for that chunk."""
