@@ -576,8 +576,9 @@ typedef struct rmda_qwen_moe_t {
 /* Device views into the scratch (byte offsets), for callers and tests:
  * p [rows][p_stride] fp32, idx/wt/slot [rows*topk], count/off [experts],
  * xp [mrows][d] fp16, amax [RMDA_QWEN_MAX_SLOTS], hp [mrows][inter] fp32
- * (the SwiGLU output; after rmda_qwen_moe_rec only the rows that hold routed
- * pairs are defined), tiles [mrows / 128] (the 128-row tile map). */
+ * (the SwiGLU output) and hp16 [mrows][inter] fp16 (its scaled cast; after
+ * rmda_qwen_moe_rec only their rows that hold routed pairs are defined),
+ * tiles [mrows / 128] (the 128-row tile map). */
 typedef struct rmda_qwen_moe_layout_t {
     size_t p;
     size_t idx;
@@ -588,6 +589,7 @@ typedef struct rmda_qwen_moe_layout_t {
     size_t xp;
     size_t amax;
     size_t hp;
+    size_t hp16;
     size_t tiles;
     size_t total;
     uint32_t p_stride;

@@ -1698,6 +1698,7 @@ int rmda_qwen_moe_layout(const rmda_qwen_moe_t *q, rmda_qwen_moe_layout_t *out) 
     out->xp = p.xp;
     out->amax = p.amax;
     out->hp = p.hp;
+    out->hp16 = p.hp16;
     out->tiles = p.tiles;
     out->total = p.total;
     out->p_stride = p.ps;

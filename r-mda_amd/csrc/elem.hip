@@ -172,15 +172,35 @@ __global__ __launch_bounds__(256) void elem4_kernel(rmda_pc_qwen_elem_t pc, cons
     }
 }
 
+// four loads in flight per thread; the maximum does not depend on the order
+// the values are taken in.  At most 256 blocks: each block ends in one
+// device atomicMax on the one slot word, and those serialise (1024 blocks:
+// config 3's 16.8 MB took 15 us)
 __global__ __launch_bounds__(256) void absmax4_kernel(const float4 *__restrict__ x, uint32_t n4,
                                                       uint32_t *__restrict__ amax, uint32_t slot) {
+    constexpr uint32_t U = 4;
+    const uint32_t st = gridDim.x * 256;
     float m = 0.0f;
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
-        const float4 v = x[i];
+    auto take = [&](const float4 &v) {
         m = fmaxf(m, fabsf(v.x));
         m = fmaxf(m, fabsf(v.y));
         m = fmaxf(m, fabsf(v.z));
         m = fmaxf(m, fabsf(v.w));
+    };
+    uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    for (; (uint64_t)i + (U - 1) * (uint64_t)st < n4; i += U * st) {
+        float4 v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            v[u] = x[i + u * st];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            take(v[u]);
+        }
+    }
+    for (; i < n4; i += st) {
+        take(x[i]);
     }
     block_absmax(m, amax, slot);
 }
@@ -202,6 +222,56 @@ __global__ __launch_bounds__(256) void cast4r_kernel(const float *__restrict__ s
             dr[c] = make_uint2((uint32_t)rmda_f2h(v.x * sc) | ((uint32_t)rmda_f2h(v.y * sc) << 16),
                                (uint32_t)rmda_f2h(v.z * sc) | ((uint32_t)rmda_f2h(v.w * sc) << 16));
         }
+    }
+}
+
+// The masked cast by tile: blocks (b, 0 .. gridDim.y - 1) take tile b of
+// the mask's row tiles, read its expert's offset and count once, and cast
+// the tile's live rows [max(lo, off), min(lo + tile, off + count))
+// (row_live's rows) between them, with four loads in flight per thread.
+// The row-strided cast4r_kernel<true> re-read the mask for every row, a
+// chain of dependent loads per row.
+__global__ __launch_bounds__(256) void cast4t_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                     uint32_t rows, uint32_t n, const uint32_t *__restrict__ amax,
+                                                     uint32_t slot, rmda_rowmask_t mk) {
+    const uint32_t e = mk.tiles[blockIdx.x];
+    if (e == RMDA_NONE) {
+        return;
+    }
+    const uint64_t lo = (uint64_t)blockIdx.x * mk.tile;
+    const uint64_t off = mk.off[e];
+    const uint64_t r0 = lo > off ? lo : off;
+    uint64_t r1 = off + mk.count[e];
+    r1 = r1 < lo + mk.tile ? r1 : lo + mk.tile;
+    r1 = r1 < rows ? r1 : rows;
+    if (r0 >= r1) {
+        return;
+    }
+    const uint32_t n4 = n / 4;
+    const uint32_t total = (uint32_t)(r1 - r0) * n4;  // float4s of the live rows, contiguous
+    const float4 *sr = reinterpret_cast<const float4 *>(src + r0 * n);
+    uint2 *dr = reinterpret_cast<uint2 *>(dst + r0 * n);
+    const float sc = cast_scale(amax, slot);
+    auto cvt = [&](const float4 &v) {
+        return make_uint2((uint32_t)rmda_f2h(v.x * sc) | ((uint32_t)rmda_f2h(v.y * sc) << 16),
+                          (uint32_t)rmda_f2h(v.z * sc) | ((uint32_t)rmda_f2h(v.w * sc) << 16));
+    };
+    constexpr uint32_t U = 4;
+    const uint32_t st = gridDim.y * 256;
+    uint32_t i = blockIdx.y * 256 + threadIdx.x;
+    for (; i + (U - 1) * st < total; i += U * st) {
+        float4 v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            v[u] = sr[i + u * st];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            dr[i + u * st] = cvt(v[u]);
+        }
+    }
+    for (; i < total; i += st) {
+        dr[i] = cvt(sr[i]);
     }
 }
 
@@ -323,6 +393,14 @@ hipError_t rmda_launch_cast_rows(hipStream_t s, uint32_t rows, uint32_t n, const
         const rmda_pc_cast_t pc{rows * n, slot};
         return rmda_launch_cast(s, &pc, src, dst, amax);
     }
+    if (mask->tile > 0 && (uint64_t)rows * n < (1ull << 32)) {
+        // blocks per row tile of the mask: about 16 float4 per thread when the tile is full
+        const uint32_t nt = (rows + mask->tile - 1) / mask->tile;
+        const uint32_t per = (mask->tile * (n / 4) + 4095) / 4096;
+        hipLaunchKernelGGL(cast4t_kernel, dim3(nt, per > 16 ? 16 : per), dim3(256), 0, s, src, dst, rows, n, amax,
+                           slot, *mask);
+        return hipGetLastError();
+    }
     rmda_pc_qwen_elem_t shape{};
     shape.rows = rows;
     shape.n = n;
@@ -333,7 +411,7 @@ hipError_t rmda_launch_cast_rows(hipStream_t s, uint32_t rows, uint32_t n, const
 hipError_t rmda_launch_absmax(hipStream_t s, const rmda_pc_absmax_t *pc, const float *x, uint32_t *amax) {
     if (pc->n % 4 == 0 && pc->n > 0 && aligned16(x)) {
         uint32_t b4 = (pc->n / 4 + 255) / 256;
-        b4 = b4 > 1024 ? 1024 : b4;
+        b4 = b4 > 256 ? 256 : b4;
         hipLaunchKernelGGL(absmax4_kernel, dim3(b4), dim3(256), 0, s, reinterpret_cast<const float4 *>(x), pc->n / 4,
                            amax, pc->slot);
         return hipGetLastError();

@@ -84,11 +84,16 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
     __shared__ uint16_t tl[MAX_TILES];
     __shared__ uint8_t tlive[LIVE ? MAX_TILES : 1];  // LIVE: rows of the compacted tile to compute, 0..RM
     __shared__ uint32_t nv_w[RMW + RIW];
+    __shared__ uint32_t swi_max, swi_done;  // SWI: the workgroup's absmax bits, MFMA waves merged
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
 
+    if (SWI && tid == 0) {
+        swi_max = 0u;
+        swi_done = 0u;
+    }
     // ---- compact the valid tiles (tiles[t] != NONE) into tl[], in order ----
     constexpr uint32_t NTH = (RMW + RIW) * RMDA_WAVE;
     const uint32_t n_all = g.max_items;
@@ -311,14 +316,22 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         }
     }
     if constexpr (SWI) {
-        // the same fmaxf of fabsf as the absmax kernels, over the wave, then
-        // one atomicMax of the bits per wave (all values non-negative)
+        // the same fmaxf of fabsf as the absmax kernels, over the wave; the
+        // MFMA waves merge theirs in LDS (an LDS atomicMax of the bits: the
+        // values are non-negative) and the last of them to arrive makes the
+        // workgroup's one device atomicMax, so the one slot word takes 256
+        // device atomics instead of one per wave
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             amx = fmaxf(amx, __shfl_xor(amx, o));
         }
-        if (lane == 0 && g.so != RMDA_NO_SLOT) {
-            atomicMax(const_cast<uint32_t *>(&g.amax[g.so]), __builtin_bit_cast(uint32_t, amx));
+        if (lane == 0) {
+            atomicMax(&swi_max, __builtin_bit_cast(uint32_t, amx));
+            // the LDS performs this wave's two atomics in order, so the wave
+            // that takes the last arrival sees every wave's maximum
+            if (atomicAdd(&swi_done, 1u) == RMW - 1 && g.so != RMDA_NO_SLOT) {
+                atomicMax(const_cast<uint32_t *>(&g.amax[g.so]), atomicMax(&swi_max, 0u));
+            }
         }
     }
 }

@@ -345,5 +345,6 @@ class QwenMoe:
             "slot": view(lay["slot"], rows * K, torch.int32),
             "amax": view(lay["amax"], 16, torch.int32),
             "hp": view(lay["hp"], mrows * q.inter, torch.float32).view(mrows, q.inter),
+            "hp16": view(lay["hp16"], mrows * q.inter, torch.float16).view(mrows, q.inter),
             "tiles": view(lay["tiles"], mrows // 128, torch.int32),
         }

@@ -138,7 +138,7 @@ def test_qwen_shim_scratch_sizing(L):
     lay = _lib.QwenLayout()
     assert L.rmda_qwen_moe_layout(ctypes.byref(q), ctypes.byref(lay)) == 0
     assert lay.total == n and lay.p_stride == E
-    offs = [lay.p, lay.idx, lay.wt, lay.count, lay.off, lay.slot, lay.xp, lay.amax, lay.hp, lay.tiles]
+    offs = [lay.p, lay.idx, lay.wt, lay.count, lay.off, lay.slot, lay.xp, lay.amax, lay.hp, lay.hp16, lay.tiles]
     assert all(o % 256 == 0 for o in offs) and len(set(offs)) == len(offs) and max(offs) < n
     # a shared expert adds the gate column to p
     q5 = _qwen(configs.CONFIGS[5], max_rows=512)

@@ -103,10 +103,11 @@ FUSED_SWIGLU = [configs.CONFIGS[2], configs.CONFIGS[3], SHAPES[3], SHAPES[4]]
 @pytest.mark.parametrize("cfg", FUSED_SWIGLU, ids=[c["name"] for c in FUSED_SWIGLU])
 def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
     """The recording's gate_up writes SwiGLU(g) and hp's absmax slot from its
-    epilogue and skips the padding rows of each 128-row segment.  On every row
-    that holds a routed pair, hp must be bitwise the public drop-ins run as
-    the reference runs them (rmda_moe_mm over the whole tiles, fp32 g, then
-    rmda_qwen_elem op 0), and the slot the absmax of those rows."""
+    epilogue and skips the padding rows of each 128-row segment, and the hp
+    cast runs over those rows only.  On every row that holds a routed pair,
+    hp and hp16 must be bitwise the public drop-ins run as the reference runs
+    them (rmda_moe_mm over the whole tiles, fp32 g, rmda_qwen_elem op 0, then
+    rmda_cast_f16 with hp's slot), and the slot the absmax of those rows."""
     print("fused swiglu %s" % cfg["name"], flush=True)
     inp = inputs.make_inputs(ctx, cfg, seed=5)
     T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
@@ -123,6 +124,7 @@ def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
         live[off[e]:off[e] + count[e]] = True
     assert live.sum() == T * K
     hp = v["hp"].cpu().numpy()[live]
+    hp16 = v["hp16"].cpu().numpy().view(np.uint16)[live]
     slots = v["amax"].clone()
     # the reference's sequence on the same xp and x slot (slot 0)
     lay = q.layout
@@ -138,6 +140,12 @@ def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
     assert bad.size == 0, "rows differ: %s" % bad[:8]
     amax = np.float32(np.abs(ref).max())
     assert slots[1].item() == int(amax.view(np.int32)), (slots[1].item(), amax)
+    hp16_ref = torch.empty(mrows, I, dtype=torch.float16, device="cuda")
+    ctx.cast_f16(mrows * I, 1, hp_ref, hp16_ref, slots)
+    ctx.sync()
+    ref16 = hp16_ref.cpu().numpy().view(np.uint16)[live]
+    bad = np.flatnonzero((hp16 != ref16).any(axis=1))
+    assert bad.size == 0, "hp16 rows differ: %s" % bad[:8]
 
 
 def test_moe_rec_runs_twice_bitwise_and_chunks(ctx):
