@@ -107,7 +107,8 @@ __global__ __launch_bounds__(256) void cast_kernel(const float *__restrict__ src
 // buffers 16-byte aligned): the same expression per element, four elements
 // per lane, a block per (column range, row stride) so no index needs a
 // division.  The absmax kernels reduce per block and merge with one
-// atomicMax per block (at most 1024 blocks).
+// atomicMax per block (at most 1024 blocks; absmax4_kernel, which keeps four
+// loads in flight per thread, at most 256).
 __device__ __forceinline__ float silu_scaled1(float g, float scale) {
     const float v = g * scale;
     return v / (1.0f + expf(-v));
