@@ -588,11 +588,12 @@ typedef struct rmda_qwen_moe_layout_t {
     size_t slot;
     size_t xp;
     size_t amax;
+    size_t total;
+    uint32_t p_stride;
+    /* added after the fields above, which keep their offsets */
     size_t hp;
     size_t hp16;
     size_t tiles;
-    size_t total;
-    uint32_t p_stride;
 } rmda_qwen_moe_layout_t;
 
 /* Scratch bytes for q's configuration and max_rows (0 when rejected). */

@@ -108,8 +108,8 @@ class QwenMoe(ctypes.Structure):
 class QwenLayout(ctypes.Structure):
     _fields_ = [("p", ctypes.c_size_t), ("idx", ctypes.c_size_t), ("wt", ctypes.c_size_t),
                 ("count", ctypes.c_size_t), ("off", ctypes.c_size_t), ("slot", ctypes.c_size_t),
-                ("xp", ctypes.c_size_t), ("amax", ctypes.c_size_t), ("hp", ctypes.c_size_t),
-                ("hp16", ctypes.c_size_t), ("tiles", ctypes.c_size_t), ("total", ctypes.c_size_t), ("p_stride", _u32)]
+                ("xp", ctypes.c_size_t), ("amax", ctypes.c_size_t), ("total", ctypes.c_size_t),
+                ("p_stride", _u32), ("hp", ctypes.c_size_t), ("hp16", ctypes.c_size_t), ("tiles", ctypes.c_size_t)]
 
 
 # name -> (restype, argtypes)
