@@ -19,6 +19,18 @@ __device__ __forceinline__ float rmda_swiglu(float g, float u) {
     return g / (1.0f + expf(-g)) * u;
 }
 
+// The fused layer's SwiGLU, in the gate_up epilogue of both GEMM tiles (one
+// expression, so the tiles agree bit for bit): the hardware exp and
+// reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each) in place of expf and
+// the IEEE division, whose instruction sequences held the MFMA waves at every
+// task's end (sustained: config 3 gate_up 156.0 -> 153.0-153.5 us, config 4
+// 113.6 -> 109.3 us).  The result is rounded to fp16, so the difference is
+// below the layer's tolerance; the reference-mode recording keeps
+// rmda_swiglu.
+__device__ __forceinline__ float rmda_swiglu_fast(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 __device__ __forceinline__ float rmda_h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }

@@ -353,7 +353,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                             for (int j = 0; j < 2; j += 1) {
                                 const float gt = acc[i][j][v];
                                 const float up = acc[i][j + 2][v];
-                                const float h = gt / (1.0f + __expf(-gt)) * up;
+                                const float h = rmda_swiglu_fast(gt, up);
                                 O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
                             }
                         }
@@ -815,7 +815,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                             for (int j = 0; j < 2; j += 1) {
                                 const float gt = acc[i][j][v];
                                 const float up = acc[i][j + 2][v];
-                                const float h = gt / (1.0f + __expf(-gt)) * up;
+                                const float h = rmda_swiglu_fast(gt, up);
                                 O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
                             }
                         }
@@ -1096,7 +1096,7 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
                         for (int j = 0; j < 2; j += 1) {
                             const float gt = acc[i][j][v];
                             const float up = acc[i][j + 2][v];
-                            const float h = gt / (1.0f + __expf(-gt)) * up;
+                            const float h = rmda_swiglu_fast(gt, up);
                             O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
                         }
                     }
