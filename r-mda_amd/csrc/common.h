@@ -163,10 +163,9 @@ __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t
                                                   float *wt_row, uint32_t *count, uint32_t *sel_row) {
     const uint32_t lane = threadIdx.x % RMDA_WAVE;
     uint32_t taken = 0;
-    // z and the per-lane output are built round by round (lane k keeps round
-    // k's selection); z still accumulates in selection order
+    // lane k keeps round k's selection; z is summed after the rounds, still
+    // in selection order
     float sv0 = 0.0f;
-    float z = 0.0f;
     uint32_t my_sel = RMDA_NONE;
     float my_val = 0.0f;
     for (uint32_t k = 0; k < topk; k += 1) {
@@ -203,11 +202,17 @@ __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t
         if (k == 0) {
             sv0 = val;
         }
-        z = z + expf(val - sv0);
         if (lane == k) {
             my_sel = col;
             my_val = val;
         }
+    }
+    // exp(l_k - l_0) once, on lane k, instead of by every lane in every
+    // round; z = ((e_0 + e_1) + e_2) + ... as the rounds added it
+    const float e = expf(my_val - sv0);
+    float z = 0.0f;
+    for (uint32_t k = 0; k < topk; k += 1) {
+        z = z + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), (int)k));
     }
     if (lane < topk) {
         if (AGENT_IDX) {
@@ -216,7 +221,7 @@ __device__ __forceinline__ void rmda_route_select(const float (&v)[NV], uint32_t
         } else {
             idx_row[lane] = my_sel;
         }
-        wt_row[lane] = expf(my_val - sv0) / z;
+        wt_row[lane] = e / z;
         if (sel_row != nullptr) {
             sel_row[lane] = my_sel;
         }
