@@ -20,27 +20,27 @@
 //   * 8 MFMA waves = 2 (M, 64 rows) x 4 (N, 64 columns),
 //     v_mfma_f32_16x16x32_f16, fp32 accumulate; they also write C.  Four more
 //     waves issue all of the DMA (4 A and 8 B instructions per stage each) and
-//     nothing else.
+//     nothing else.  On gfx950 a wave's stores count in vmcnt like its
+//     loads, so a wave that both streamed the stages and wrote a finished
+//     tile's 128 KiB of fp32 C would drain its whole load pipeline at every
+//     wait after a tile; measured at T = 2048, 128 experts, top-8, the stores
+//     then cost gate_up 122 of 327 us.  With the split the issue waves' waits
+//     count their own loads only (gate_up 327 -> 260 us), and C goes out with
+//     non-temporal stores, written once and not read again here
+//     (260 -> 247 us).
 //   * LIVE (the recording's own calls, rmda_gemm_args_t::live_count): a
 //     tile's rows past its segment's routed rows are padding whose results
 //     nothing reads, so 16-row groups wholly past them run no MFMAs (a wave
 //     whose 64 rows are all padding reads no fragments either), their rows
 //     are not stored, and their A loads read the tile's first row again
-//     instead of HBM.  At config 3 a third of the used tiles' rows are
-//     padding.
+//     instead of HBM.  At T = 2048, 128 experts, top-8 a third of the used
+//     tiles' rows are padding.
 //   * SWI (rmda_gemm_args_t::f32_swiglu, the recording's gate_up): the N
 //     tile is 128 gate columns j and their 128 up columns n_w/2 + j, laid out
 //     so that each MFMA wave holds 32 of each for the same 32 outputs (LDS
 //     rows 64w .. 64w+31 gate, 64w+32 .. 64w+63 up); the epilogue writes
 //     silu(g) * u in place of the two fp32 columns and folds the absmax
-//     that the next cast needs, so C never goes to memory.  On gfx950 a wave's stores count in vmcnt like its loads,
-//     so a wave that both streamed the stages and wrote a finished tile's
-//     128 KiB of fp32 C would drain its whole load pipeline at every wait
-//     after a tile; measured at BASELINE config 3, the stores then cost
-//     gate_up 122 of 327 us.  With the split the issue waves' waits count
-//     their own loads only (gate_up 327 -> 260 us), and C goes out with
-//     non-temporal stores, written once and not read again here
-//     (260 -> 247 us).
+//     that the next cast needs, so C never goes to memory.
 #include "common.h"
 #include "gemm_sched.h"
 
