@@ -34,6 +34,19 @@
 extern "C" {
 #endif
 
+/* Version of this header's binary interface.  It changes whenever a struct
+ * the caller passes in or the library fills grows or changes layout (no
+ * counterpart in the reference, which links its kernels statically).  A
+ * caller checks rmda_moe_abi_version() == RMDA_MOE_ABI_VERSION once at load
+ * time; on a mismatch it was built against another header and must be
+ * rebuilt, since the library may read or write past its structs.
+ *   1  the first release;
+ *   2  rmda_moe_ws_layout_t gained items / n_items / n_items_hot and
+ *      rmda_qwen_moe_layout_t gained hp / hp16 / tiles;
+ *   3  rmda_moe_layer_args_t gained x32 (fp32 activations with a slot
+ *      scale). */
+#define RMDA_MOE_ABI_VERSION 3
+
 /* Same value as MDA_PC_NO_SLOT (src/pc.h:6): "no fp16 scale slot". */
 #define RMDA_NO_SLOT 0xffffffffu
 /* Sentinel for an unused tile / a pair with no selectable expert. */
@@ -156,18 +169,33 @@ int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows);
  *   RMDA_TILE_AUTO      launches both tiles every call; the one whose list
  *                       the rank kernel left empty exits at once (about
  *                       4 us per launch on MI355X);
- *   RMDA_TILE_ADAPTIVE  (default) launches only the tile the context's
- *                       previous call chose (the rank kernel reports its
- *                       choice to a host-visible word) and makes the rank
- *                       kernel cut its list for that tile; the first call,
- *                       and the first after rmda_moe_set_hot_rows or this
- *                       function, runs as AUTO;
+ *   RMDA_TILE_ADAPTIVE  (default) launches only the tile that the
+ *                       context's previous call on the same packed weights
+ *                       and row count chose (the rank kernel reports its
+ *                       choice to a host-visible word of a 64-entry table
+ *                       keyed by those two) and makes the rank kernel cut
+ *                       its list for that tile; the first call of a key
+ *                       (and of a key whose entry another key took since),
+ *                       and every call after rmda_moe_set_hot_rows or this
+ *                       function, runs as AUTO until its choice lands;
  *   RMDA_TILE_STREAM / RMDA_TILE_HOT  always that tile.
  * Every policy gives bitwise the same output; calls with rows < hot rows
  * (no expert can be hot) and HF-layout weights launch the streaming tile
  * only. */
 enum { RMDA_TILE_ADAPTIVE = 0, RMDA_TILE_AUTO = 1, RMDA_TILE_STREAM = 2, RMDA_TILE_HOT = 3 };
 int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy);
+/* Route inside the rank launch for calls of more than one rank block of
+ * 1024 (token, expert) pairs, up to 65536 pairs: the
+ * launches before gate_up are then the router and one rank launch, in which
+ * one workgroup per 8 tokens selects the top-k as moe_route does
+ * (shader/moe_route.comp:20-61, dispatched at src/qwen.c:799-811) and the
+ * workgroups that finish last rank the pairs, after a device-scope
+ * release/acquire ticket.  Off by default: slower on MI355X (config 3 layer
+ * 308.0 -> 310-312 us, config 5 815 -> 818-821 us), because that hand-off
+ * costs more than the kernel boundary it replaces.  Calls of one rank block
+ * (decode sizes) always route in the rank launch.  Every setting gives
+ * bitwise the same results. */
+int rmda_moe_set_route_in_rank(rmda_moe_ctx_t *ctx, int on);
 /* Fold the combine into the down GEMM (replaces moe_combine's own dispatch,
  * src/qwen.c:887-906, inside rmda_moe_layer; off by default).  Each down-GEMM
  * wave that stores the last of a token's rows for 64 output columns sums
@@ -187,6 +215,8 @@ void rmda_moe_ctx_clear_error(rmda_moe_ctx_t *ctx);
 int rmda_moe_sync(rmda_moe_ctx_t *ctx);
 /* Library version string and the gfx target it was built for. */
 const char *rmda_moe_version(void);
+/* RMDA_MOE_ABI_VERSION of the header the library was built with. */
+int rmda_moe_abi_version(void);
 
 /* ---- per-stage drop-ins (one per reference kernel, buffers in binding order) ---- */
 
@@ -218,8 +248,10 @@ int rmda_moe_scan(rmda_moe_ctx_t *ctx, const rmda_pc_moe_scan_t *pc,
  * idx RMDA_NONE get slot RMDA_NONE and copy nothing.  `fill` is scratch of
  * `experts` words: treated as zero on entry, left holding the per-expert
  * counts (what the reference's atomics leave there).  Rows of xp that no pair
- * targets are not written (the reference zero-fills them first,
- * src/qwen.c:798; rmda_moe_mm never reads them as valid data).
+ * targets are not written: a caller that runs rmda_moe_mm on xp next must
+ * zero-fill xp first, as the reference does (src/qwen.c:798), because
+ * rmda_moe_mm computes every row of each tile the map names, the segments'
+ * padding rows included.
  * `experts` is taken from the context's last rmda_moe_route call unless set
  * with rmda_moe_scatter_experts().  Requires rows*topk <= RMDA_CTX_MAX_PAIRS
  * and 16-byte aligned x16 and xp. */
@@ -313,7 +345,7 @@ typedef struct rmda_moe_shape_t {
  * aligned, bias and inj 4-byte aligned (RMDA_ERR_ARG otherwise), like the
  * reference's storage-buffer offsets. */
 typedef struct rmda_moe_layer_args_t {
-    const uint16_t *x;          /* rows x d fp16 activations */
+    const uint16_t *x;          /* rows x d fp16 activations, or NULL when x32 is given */
     const float *w_router;      /* (experts [+1 shared gate]) x d fp32 */
     const float *bias;          /* experts fp32 router bias, or NULL */
     const uint16_t *w_gate_up;  /* [experts][2*inter][d] fp16: gate rows then up rows */
@@ -336,6 +368,19 @@ typedef struct rmda_moe_layer_args_t {
     uint32_t inj_stride;
     uint32_t inj_off;
     uint32_t hc;                /* 1 .. 8 streams (the reference uses 4) */
+    /* fp32 activations (the chunk's sc->x, src/qwen.c:844), in place of x
+     * (exactly one of the two is given).  The layer then runs the reference's
+     * fp16 scale-slot protocol (src/qwen.c:500-539): x's absmax goes into a
+     * fresh slot and x is cast to fp16 times 2^(141 - exponent(absmax))
+     * (absmax.comp, cast_f16.comp), which the router and gate_up divide out;
+     * the SwiGLU output is kept in fp32 and cast with a slot of its own
+     * (src/qwen.c:858-877), which down divides out; and down's rows stay
+     * fp32 up to the combine (src/qwen.c:878).  So activations far outside
+     * fp16's range (say 1e-6 or 1e6) route and multiply as in the reference.
+     * For inputs that are fp16 values in fp16's normal range the routing is
+     * bitwise that of x = those values.  Needs rmda_moe_workspace_bytes_x32
+     * of workspace; the combine is never folded into down in this mode. */
+    const float *x32;
 } rmda_moe_layer_args_t;
 
 /* Device views into the workspace after rmda_moe_layer (byte offsets), so a
@@ -359,6 +404,10 @@ typedef struct rmda_moe_ws_layout_t {
 } rmda_moe_ws_layout_t;
 
 size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape);
+/* Workspace of rmda_moe_layer with args->x32 set: the scaled fp16 copy of x
+ * and the fp32 SwiGLU output / expert rows on top of the above (config 3:
+ * 112.9 MB against 104.5 MB). */
+size_t rmda_moe_workspace_bytes_x32(const rmda_moe_shape_t *shape);
 int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_t *out);
 
 /* The whole layer: router -> route -> scan -> permutation -> grouped SwiGLU
@@ -382,8 +431,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
  * args->workspace_bytes 0: the workspace is the library's static device array
  * of RMDA_STATIC_WS_BYTES, one per device, reserved when the code object is
  * loaded and held until the process ends.  Shapes whose
- * rmda_moe_workspace_bytes exceeds it fail with RMDA_ERR_CAPACITY (config 3,
- * T=2048 x d=2048 x 128 experts top-8, needs 104.5 MB).  The call allocates
+ * rmda_moe_workspace_bytes (with x32: rmda_moe_workspace_bytes_x32) exceeds
+ * it fail with RMDA_ERR_CAPACITY (config 3, T=2048 x d=2048 x 128 experts
+ * top-8, needs 104.5 MB).  The call allocates
  * nothing and enqueues only kernels (the rank ticket it needs zeroed is
  * cleared by the router kernel).  Every call on a device shares that device's
  * array and leaves its contents behind, so calls that overlap on one device

@@ -224,6 +224,7 @@ typedef struct {
     const uint16_t *x16;
     const float *wt; /* [cols][L][8] interleaved chunks */
     const float *bias;
+    float post;      /* applied to the chunk sum before the bias (1/slot scale) */
     float *proj;
 } orc_router_job_t;
 
@@ -253,6 +254,7 @@ static void orc_router_row(void *vctx, uint64_t r) {
         for (int q = 1; q < 8; q += 1) {
             s = s + p[q];
         }
+        s = s * j->post;
         if (j->bias != NULL && c < j->pc->nbias) {
             s = s + j->bias[c];
         }
@@ -263,6 +265,14 @@ static void orc_router_row(void *vctx, uint64_t r) {
 
 void orc_router(const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
                 const float *bias, float *proj, int threads) {
+    orc_router_scaled(pc, x16, w, bias, 1.0f, proj, threads);
+}
+
+/* The same with every chunk sum multiplied by `post` before the bias: the
+ * router on a slot-scaled x16 with 1/scale as post (the reference divides
+ * the scale out in the GEMM's epilogue, shader/matmul_f16.comp's scale). */
+void orc_router_scaled(const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
+                       const float *bias, float post, float *proj, int threads) {
     uint32_t d = pc->d;
     uint32_t L = d / 8;
     float *wt = malloc(sizeof(float) * (size_t)pc->cols * d);
@@ -273,7 +283,7 @@ void orc_router(const rmda_moe_router_t *pc, const uint16_t *x16, const float *w
             }
         }
     }
-    orc_router_job_t j = {.pc = pc, .x16 = x16, .wt = wt, .bias = bias, .proj = proj};
+    orc_router_job_t j = {.pc = pc, .x16 = x16, .wt = wt, .bias = bias, .post = post, .proj = proj};
     orc_parallel(pc->rows, orc_router_row, &j, threads);
     free(wt);
 }
@@ -728,9 +738,30 @@ int orc_moe_layer(const orc_layer_t *L) {
         st[i] += t_now - t_mark;       \
         t_mark = t_now;                \
     } while (0)
+    /* activations fed to the GEMMs: x, optionally power-of-two scaled
+     * (src/qwen.c:844; bit-neutral for in-range values); with fp32 x32 always
+     * scaled, as the reference casts its fp32 sc->x, and the router reads the
+     * same cast with the scale divided out */
+    size_t xn = (size_t)T * d;
+    uint16_t *a16 = malloc(sizeof(uint16_t) * xn + 2);
+    float sa = 1.0f;
+    if (L->x32 != NULL) {
+        sa = orc_scaled_cast(L->x32, a16, xn, 1);
+    } else if (L->x_scale) {
+        float *xf = malloc(sizeof(float) * xn + 4);
+        orc_h2f_n(L->x, xf, xn);
+        sa = orc_scaled_cast(xf, a16, xn, 1);
+        free(xf);
+    } else {
+        memcpy(a16, L->x, sizeof(uint16_t) * xn);
+    }
     /* A0: router projection (x . [W_router; w_shared_gate]^T), canonical order */
     rmda_moe_router_t pr = {.rows = T, .d = d, .cols = ps, .stride = ps, .nbias = E};
-    orc_router(&pr, L->x, L->w_router, L->bias, proj, th);
+    if (L->x32 != NULL) {
+        orc_router_scaled(&pr, a16, L->w_router, L->bias, sa, proj, th);
+    } else {
+        orc_router(&pr, L->x, L->w_router, L->bias, proj, th);
+    }
     ORC_STAGE(0);
     /* A1-A3: route, scan, scatter (slots only; the GEMMs read token rows) */
     rmda_pc_moe_route_t pc_r = {.rows = T, .experts = E, .topk = K, .stride = ps};
@@ -743,19 +774,6 @@ int orc_moe_layer(const orc_layer_t *L) {
     orc_moe_scatter(&pc_t, idx, off, fill, NULL, NULL, slot);
     ORC_STAGE(3);
 
-    /* activations fed to the GEMMs: x, optionally power-of-two scaled
-     * (src/qwen.c:844; bit-neutral for in-range values) */
-    size_t xn = (size_t)T * d;
-    uint16_t *a16 = malloc(sizeof(uint16_t) * xn + 2);
-    float sa = 1.0f;
-    if (L->x_scale) {
-        float *xf = malloc(sizeof(float) * xn + 4);
-        orc_h2f_n(L->x, xf, xn);
-        sa = orc_scaled_cast(xf, a16, xn, 1);
-        free(xf);
-    } else {
-        memcpy(a16, L->x, sizeof(uint16_t) * xn);
-    }
 
     /* selected tokens and their pairs */
     uint32_t n_tok = L->rows_sel ? L->n_sel : T;

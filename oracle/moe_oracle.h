@@ -44,6 +44,9 @@ void orc_fill_normal_f32(float *dst, size_t n, uint64_t stream, uint64_t seed, f
  * right, then the bias). */
 void orc_router(const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
                 const float *bias, float *proj, int threads);
+/* orc_router with each chunk sum multiplied by post before the bias */
+void orc_router_scaled(const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
+                       const float *bias, float post, float *proj, int threads);
 
 /* shader/moe_route.comp, generalised (only columns < experts are read). */
 void orc_moe_route(const rmda_pc_moe_route_t *pc, const float *proj, uint32_t *idx,
@@ -114,6 +117,11 @@ typedef struct orc_layer_t {
      * router, route, scan, scatter, gate_up (+SwiGLU, cast), down, shared
      * expert, combine (ORC_LAYER_STAGES) */
     double *stage_ms;
+    /* or NULL: fp32 activations in place of x (x may then be NULL), cast to
+     * fp16 with a slot scale for the router and the GEMMs as the reference
+     * casts its fp32 chunk (src/qwen.c:517-539, :844); the router divides the
+     * scale out before the bias */
+    const float *x32;
 } orc_layer_t;
 #define ORC_LAYER_STAGES 8
 

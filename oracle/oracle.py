@@ -71,7 +71,7 @@ class Layer(ctypes.Structure):
                 ("x", _p), ("w_router", _p), ("bias", _p), ("w_gate_up", _p), ("w_down", _p),
                 ("w_sh_gate_up", _p), ("w_sh_down", _p), ("rows_sel", _p), ("n_sel", _u32),
                 ("out", _p), ("proj", _p), ("idx", _p), ("wt", _p), ("slot", _p), ("count", _p),
-                ("off", _p), ("ye16", ctypes.c_int), ("stage_ms", _p)]
+                ("off", _p), ("ye16", ctypes.c_int), ("stage_ms", _p), ("x32", _p)]
 
 LAYER_STAGES = ("router", "route", "scan", "scatter", "gate_up", "down", "shared", "combine")
 
@@ -289,7 +289,8 @@ def layer(inp, tile=1, hp_scale=1, x_scale=1, rows_sel=None, threads=None, ye16=
     """Whole layer in the reference order (plain output, fp32).
 
     `inp` is a dict of host numpy arrays (see rmda_moe.inputs): x, w_router,
-    bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down and the shape fields.
+    bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down and the shape fields;
+    an fp32 "x32" in place of x runs the reference's slot-scaled cast of x.
     ye16 rounds every expert output row to fp16 before the combine (the
     fused GPU layer's storage).  Returns a dict with out, the routing
     intermediates and stage_ms (wall-clock ms per stage, LAYER_STAGES).
@@ -322,6 +323,7 @@ def layer(inp, tile=1, hp_scale=1, x_scale=1, rows_sel=None, threads=None, ye16=
     L.shape = Shape(T, d, E, K, s["inter"], s["shared"])
     L.tile, L.hp_scale, L.x_scale, L.threads = tile, hp_scale, x_scale, _nthreads(threads)
     L.x, L.w_router, L.bias = P("x"), P("w_router"), P("bias")
+    L.x32 = P("x32")  # fp32 activations (then x may be None)
     L.w_gate_up, L.w_down = P("w_gate_up"), P("w_down")
     L.w_sh_gate_up, L.w_sh_down = P("w_sh_gate_up"), P("w_sh_down")
     L.rows_sel = _ptr(sel)

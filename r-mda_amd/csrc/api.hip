@@ -15,6 +15,8 @@
 
 #include "common.h"
 
+constexpr uint32_t kHintSlots = 64;
+
 struct rmda_moe_ctx {
     int device;
     hipStream_t stream;
@@ -37,14 +39,22 @@ struct rmda_moe_ctx {
     int hot_stages;
     int hot_sched;
     // tile policy (RMDA_TILE_*; RMDA_MOE_TILE_POLICY overrides, tuning only)
-    // and the word the rank kernel reports its tile choice to (pinned host
-    // memory, mapped into the device)
+    // and the words the rank kernel reports its tile choice to (pinned host
+    // memory, mapped into the device): one per (packed weights, rows) key in
+    // a small direct-mapped table, so that a context serving many layers
+    // reads each layer's own last choice
     int tile_policy;
-    uint32_t *tile_hint_host;
+    uint32_t *tile_hint_host;  // [kHintSlots]
     uint32_t *tile_hint_dev;
+    const void *hint_key_w[kHintSlots];
+    uint32_t hint_key_rows[kHintSlots];
     // combine folded into the down GEMM (rmda_moe_set_fused_combine;
     // RMDA_MOE_FUSED_COMBINE sets the initial value)
     int fused_combine;
+    // top-k folded into the rank launch above one rank block
+    // (rmda_moe_set_route_in_rank; RMDA_MOE_ROUTE_IN_RANK sets the initial
+    // value); one rank block always routes in the rank launch
+    int route_rank;
     // stage profiler: a ring of per-call event sets, harvested when full
     int prof_on;
     int prof_made;
@@ -128,6 +138,36 @@ size_t align256(size_t x) {
     return (x + 255) & ~(size_t)255;
 }
 
+// Tile-choice hints of RMDA_TILE_ADAPTIVE: forget every key and choice.
+void hint_clear(rmda_moe_ctx_t *c) {
+    for (uint32_t i = 0; i < kHintSlots; i += 1) {
+        c->hint_key_w[i] = nullptr;
+        c->hint_key_rows[i] = 0;
+        __atomic_store_n(&c->tile_hint_host[i], 0u, __ATOMIC_RELAXED);
+    }
+}
+
+// The hint slot of a call on weights w with `rows` tokens, and the tile the
+// last call with the same key chose (1 streaming, 2 compute), or 0 when the
+// slot held another key (then claimed for this one) or no choice has landed
+// yet.  A kernel of the slot's previous key still in flight may store its
+// choice after the claim; that costs one call the other tile, never a
+// different result (both tiles give the same bits).
+uint32_t hint_lookup(rmda_moe_ctx_t *c, const void *w, uint32_t rows, uint32_t *slot) {
+    const uint64_t h = ((uint64_t)reinterpret_cast<uintptr_t>(w) >> 8) * 0x9E3779B97F4A7C15ull ^
+                       (uint64_t)rows * 0xC2B2AE3D27D4EB4Full;
+    const uint32_t i = (uint32_t)(h >> 58) % kHintSlots;
+    *slot = i;
+    if (c->hint_key_w[i] == w && c->hint_key_rows[i] == rows) {
+        const uint32_t v = __atomic_load_n(&c->tile_hint_host[i], __ATOMIC_RELAXED);
+        return v == 1u || v == 2u ? v : 0u;
+    }
+    c->hint_key_w[i] = w;
+    c->hint_key_rows[i] = rows;
+    __atomic_store_n(&c->tile_hint_host[i], 0u, __ATOMIC_RELAXED);
+    return 0u;
+}
+
 const char *const kStageNames[RMDA_PROF_STAGES] = {"router", "route", "rank", "permute",
                                                    "gate_up", "down", "combine"};
 
@@ -193,8 +233,8 @@ void prof_skip(rmda_moe_ctx_t *c, uint32_t st) {
 }
 
 struct LayerPlan {
-    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, ye, fc_cnt,
-        total;
+    size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, fc_cnt, xs16,
+        xpart, xslot, hslot, ye, total;
     uint32_t ps, npairs, nblocks, max_items, sh_rows, sh_row0, groups_rows;
 };
 
@@ -226,7 +266,12 @@ int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
     return 1;
 }
 
-LayerPlan plan_layer(const rmda_moe_shape_t *s) {
+// x32: the slot-scaled mode (fp32 activations): the scaled fp16 copy of x,
+// the absmax parts and two slot words, and a last region that holds first
+// the fp32 SwiGLU output (hp32) and then the fp32 expert rows (ye32), where
+// the default mode's is the fp16 ye.  Every offset but that of the last
+// region's end is the same in both modes.
+LayerPlan plan_layer(const rmda_moe_shape_t *s, bool x32 = false) {
     LayerPlan p{};
     const uint32_t T = s->rows;
     const uint32_t K = s->topk;
@@ -263,9 +308,13 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s) {
     // are never more than the streaming tile's
     p.items = take((size_t)p.max_items * 16);
     p.hp = take((size_t)p.groups_rows * s->inter * 2);
-    p.ye = take((size_t)p.groups_rows * s->d * 2);
     // arrival counters of the folded combine, one per (token, 64 columns)
     p.fc_cnt = take((size_t)T * (s->d / RMDA_FC_COLS) * 4);
+    p.xs16 = take(x32 ? (size_t)T * s->d * 2 : 0);
+    p.xpart = take(x32 ? (size_t)RMDA_XCAST_PARTS * 4 : 0);
+    p.xslot = take(x32 ? 4 : 0);
+    p.hslot = take(x32 ? 4 : 0);
+    p.ye = take(x32 ? (size_t)p.groups_rows * std::max(s->d, s->inter) * 4 : (size_t)p.groups_rows * s->d * 2);
     p.total = o;
     return p;
 }
@@ -300,7 +349,11 @@ T *at(void *base, size_t off) {
 extern "C" {
 
 const char *rmda_moe_version(void) {
-    return "rmda_moe 0.1 (gfx950, wave64, fp16 MFMA)";
+    return "rmda_moe 0.3 (gfx950, wave64, fp16 MFMA)";
+}
+
+int rmda_moe_abi_version(void) {
+    return RMDA_MOE_ABI_VERSION;
 }
 
 int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
@@ -376,6 +429,10 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
     if (const char *v = getenv("RMDA_MOE_HOT_SCHED")) {
         c->hot_sched = atoi(v);
     }
+    c->route_rank = 0;
+    if (const char *v = getenv("RMDA_MOE_ROUTE_IN_RANK")) {
+        c->route_rank = atoi(v) != 0 ? 1 : 0;
+    }
     c->fused_combine = 0;
     if (const char *v = getenv("RMDA_MOE_FUSED_COMBINE")) {
         c->fused_combine = atoi(v) != 0 ? 1 : 0;
@@ -385,13 +442,14 @@ int rmda_moe_ctx_create(rmda_moe_ctx_t **out, int device, void *stream) {
         const int pol = atoi(v);
         c->tile_policy = pol >= RMDA_TILE_ADAPTIVE && pol <= RMDA_TILE_HOT ? pol : RMDA_TILE_ADAPTIVE;
     }
-    if (hipHostMalloc(reinterpret_cast<void **>(&c->tile_hint_host), 64, hipHostMallocMapped) != hipSuccess ||
+    if (hipHostMalloc(reinterpret_cast<void **>(&c->tile_hint_host), kHintSlots * 4, hipHostMallocMapped) !=
+            hipSuccess ||
         hipHostGetDevicePointer(reinterpret_cast<void **>(&c->tile_hint_dev), c->tile_hint_host, 0) != hipSuccess) {
         (void)hipFree(c->fixed_ws);
         delete c;
         return RMDA_ERR_HIP;
     }
-    __atomic_store_n(c->tile_hint_host, 0u, __ATOMIC_RELAXED);
+    hint_clear(c);
     if (prev >= 0 && prev != device) {
         (void)hipSetDevice(prev);
     }
@@ -502,7 +560,7 @@ int rmda_moe_set_hot_rows(rmda_moe_ctx_t *ctx, uint32_t rows) {
         return RMDA_ERR_ARG;
     }
     ctx->hot_min = rows;
-    __atomic_store_n(ctx->tile_hint_host, 0u, __ATOMIC_RELAXED);  // the next call chooses afresh
+    hint_clear(ctx);  // the next call on every layer chooses afresh
     return RMDA_OK;
 }
 
@@ -511,7 +569,15 @@ int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy) {
         return RMDA_ERR_ARG;
     }
     ctx->tile_policy = policy;
-    __atomic_store_n(ctx->tile_hint_host, 0u, __ATOMIC_RELAXED);
+    hint_clear(ctx);
+    return RMDA_OK;
+}
+
+int rmda_moe_set_route_in_rank(rmda_moe_ctx_t *ctx, int on) {
+    if (ctx == nullptr) {
+        return RMDA_ERR_ARG;
+    }
+    ctx->route_rank = on != 0 ? 1 : 0;
     return RMDA_OK;
 }
 
@@ -865,6 +931,17 @@ size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape) {
     return plan_layer(shape).total;
 }
 
+size_t rmda_moe_workspace_bytes_x32(const rmda_moe_shape_t *shape) {
+    if (shape == nullptr) {
+        return 0;
+    }
+    char why[128];
+    if (!check_shape(shape, why, sizeof(why))) {
+        return 0;
+    }
+    return plan_layer(shape, true).total;
+}
+
 int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_t *out) {
     if (shape == nullptr || out == nullptr) {
         return RMDA_ERR_ARG;
@@ -911,11 +988,14 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     if (rc != RMDA_OK) {
         return rc;
     }
-    if (shape == nullptr || args == nullptr || args->x == nullptr ||
+    if (shape == nullptr || args == nullptr || (args->x == nullptr && args->x32 == nullptr) ||
         (args->packed == nullptr && (args->w_router == nullptr || args->w_gate_up == nullptr ||
                                      args->w_down == nullptr)) ||
         (args->out == nullptr && args->h == nullptr) || args->workspace == nullptr) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: null argument");
+    }
+    if (args->x != nullptr && args->x32 != nullptr) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: give x (fp16) or x32 (fp32), not both");
     }
     if (args->h != nullptr &&
         (args->inj == nullptr || args->hc == 0 || args->hc > RMDA_MAX_HC || args->inj_stride < args->inj_off + args->hc)) {
@@ -926,7 +1006,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     if (!aligned(args->x, 16) || !aligned(args->w_router, 16) || !aligned(args->w_gate_up, 16) ||
         !aligned(args->w_down, 16) || !aligned(args->w_sh_gate_up, 16) || !aligned(args->w_sh_down, 16) ||
         !aligned(args->packed, 16) || !aligned(args->out, 16) || !aligned(args->workspace, 16) ||
-        !aligned(args->h, 16) || !aligned(args->bias, 4) || !aligned(args->inj, 4)) {
+        !aligned(args->h, 16) || !aligned(args->x32, 16) || !aligned(args->bias, 4) || !aligned(args->inj, 4)) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: x, weights, out, h and workspace must be 16-byte aligned");
     }
     char why[128];
@@ -937,10 +1017,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         (args->w_sh_gate_up == nullptr || args->w_sh_down == nullptr)) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_layer: shared expert weights missing");
     }
-    const LayerPlan p = plan_layer(shape);
+    // fp32 activations: the reference's slot-scaled casts (see rmda_moe_layer_args_t::x32)
+    const bool x32 = args->x32 != nullptr;
+    const LayerPlan p = plan_layer(shape, x32);
     if (args->workspace_bytes < p.total) {
-        return fail(ctx, RMDA_ERR_WORKSPACE, "rmda_moe_layer: workspace %zu bytes < %zu", args->workspace_bytes,
-                    p.total);
+        return fail(ctx, RMDA_ERR_WORKSPACE, "rmda_moe_layer: workspace %zu bytes < %zu%s", args->workspace_bytes,
+                    p.total, x32 ? " (rmda_moe_workspace_bytes_x32)" : "");
     }
     if (shape->rows == 0) {
         return RMDA_OK;
@@ -961,6 +1043,10 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     uint32_t *done = at<uint32_t>(ws, p.done);
     uint16_t *hp = at<uint16_t>(ws, p.hp);
     uint16_t *ye = at<uint16_t>(ws, p.ye);
+    // the activations the router and gate_up read, and (x32) the two slots
+    const uint16_t *xin = x32 ? at<uint16_t>(ws, p.xs16) : args->x;
+    uint32_t *xslot = x32 ? at<uint32_t>(ws, p.xslot) : nullptr;
+    uint32_t *hslot = x32 ? at<uint32_t>(ws, p.hslot) : nullptr;
     const uint16_t *packed = args->packed;
     const PackPlan pk = plan_pack(shape);
     const uint16_t *w_gu = packed != nullptr ? packed + pk.gate_up : args->w_gate_up;
@@ -976,24 +1062,41 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         }
     }
     rc = prof_mark(ctx, 0);
+    // fp32 activations: x's absmax into a fresh slot and the scaled fp16 cast
+    // the router and gate_up read (absmax.comp + cast_f16.comp,
+    // src/qwen.c:517-539, :844); the second launch also clears hp's slot
+    if (rc == RMDA_OK && x32) {
+        rc = hip_check(ctx, rmda_launch_x_absmax(s, args->x32, (size_t)T * d, at<uint32_t>(ws, p.xpart)),
+                       "layer x absmax");
+        if (rc == RMDA_OK) {
+            rc = hip_check(ctx,
+                           rmda_launch_x_cast(s, args->x32, (size_t)T * d, at<uint32_t>(ws, p.xpart),
+                                              at<uint16_t>(ws, p.xs16), xslot, hslot),
+                           "layer x cast");
+        }
+    }
     // A0 router projection (+ zero the rank ticket for this call) with the A1
     // top-k fused in when one workgroup can hold a token's whole logit row
     const bool fuse_route = p.ps <= rmda_route_fuse_max_cols();
     rmda_route_fuse_t fz{E, K, idx, wt};
     if (rc == RMDA_OK) {
         rc = hip_check(ctx,
-                       rmda_launch_router(s, args->x, w_rt, packed != nullptr, args->bias, proj, T, d, p.ps,
-                                          p.ps, args->bias != nullptr ? E : 0, done, 1,
-                                          fuse_route ? &fz : nullptr),
+                       rmda_launch_router(s, xin, w_rt, packed != nullptr, args->bias, proj, T, d, p.ps, p.ps,
+                                          args->bias != nullptr ? E : 0, done, 1, fuse_route ? &fz : nullptr,
+                                          xslot),
                        "layer router");
     }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_ROUTER + 1);
     }
-    // A1 top-k (unless fused above).  When every pair fits one rank block
-    // (decode sizes), the rank kernel routes the rows itself, so the chain
-    // before gate_up is two launches (router, rank) instead of three.
-    const bool route_in_rank = !fuse_route && p.nblocks == 1;
+    // A1 top-k (unless fused above).  The rank kernel routes the rows itself
+    // when its blocks can rank without a hand-off of block totals (one rank
+    // block, or up to RMDA_RANK_ALL_MAX pairs, where every rank block counts
+    // every pair), so the chain before gate_up is two launches (router, rank)
+    // instead of three.
+    const bool self_perm = p.nblocks == 1 ||
+                           (p.npairs <= RMDA_RANK_ALL_MAX && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0);
+    const bool route_in_rank = !fuse_route && self_perm && (ctx->route_rank != 0 || p.nblocks == 1);
     if (rc == RMDA_OK && !fuse_route && !route_in_rank) {
         rc = hip_check(ctx, rmda_launch_route(s, proj, idx, wt, nullptr, T, E, K, p.ps), "layer route");
         if (rc == RMDA_OK) {
@@ -1007,23 +1110,21 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     // with fewer rows than hot_min (a token adds at most one row per expert).
     const bool hot_possible = packed != nullptr && ctx->hot_min > 0 && T >= ctx->hot_min;
     uint32_t tile_mode = 1;
+    uint32_t hint_slot = 0;
     if (hot_possible) {
         switch (ctx->tile_policy) {
         case RMDA_TILE_STREAM: tile_mode = 1; break;
         case RMDA_TILE_HOT: tile_mode = 2; break;
         case RMDA_TILE_AUTO: tile_mode = 0; break;
-        default: {
-            const uint32_t h = __atomic_load_n(ctx->tile_hint_host, __ATOMIC_RELAXED);
-            tile_mode = h == 1u || h == 2u ? h : 0u;
-        }
+        default: tile_mode = hint_lookup(ctx, packed, T, &hint_slot);
         }
     }
     // The combine folds into the down GEMM when the streaming tile runs it on
     // packed weights; when the compute tile may run instead, combine16_kernel
     // is enqueued too and does the combine only if that tile ran.
-    const bool fold_combine = ctx->fused_combine != 0 && packed != nullptr && ctx->g2.spec != 0 && tile_mode != 2u;
+    const bool fold_combine =
+        ctx->fused_combine != 0 && packed != nullptr && ctx->g2.spec != 0 && tile_mode != 2u && !x32;
     // A2 counts, offsets, block bases and the GEMM work list
-    bool self_perm = false;
     if (rc == RMDA_OK) {
         rmda_rank_args_t ra{};
         ra.idx = idx;
@@ -1044,7 +1145,8 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         ra.bm_hot = RMDA_GEMM_HOT_BM;
         ra.hot_min = hot_possible ? ctx->hot_min : 0u;
         ra.force = tile_mode;
-        ra.hint_out = ctx->tile_policy == RMDA_TILE_ADAPTIVE && hot_possible ? ctx->tile_hint_dev : nullptr;
+        ra.hint_out =
+            ctx->tile_policy == RMDA_TILE_ADAPTIVE && hot_possible ? ctx->tile_hint_dev + hint_slot : nullptr;
         ra.shared_rows = p.sh_rows;
         ra.shared_row0 = p.sh_row0;
         // all pairs in one rank block, or few enough pairs that every block
@@ -1065,8 +1167,6 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
             ra.fc_zero_out = args->out;
             ra.fc_d = d;
         }
-        self_perm = p.nblocks == 1 ||
-                    (p.npairs <= RMDA_RANK_ALL_MAX && (reinterpret_cast<uintptr_t>(idx) & 15u) == 0);
         if (self_perm) {
             ra.slot = slot;
             ra.rowtok = rowtok;
@@ -1101,7 +1201,10 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     // A4-A6 gate_up with SwiGLU epilogue -> hp16
     if (rc == RMDA_OK) {
         g.mode = RMDA_GEMM_SWIGLU;
-        g.a = args->x;
+        g.a = xin;
+        g.xscale = xslot;
+        g.hp32 = x32 ? at<float>(ws, p.ye) : nullptr;  // fp32 SwiGLU output, cast below
+        g.hp_amax = hslot;
         g.rowtok = rowtok;
         g.a_rows = T;
         g.lda = d;
@@ -1126,6 +1229,13 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         // the list for it), then the streaming tile (work only otherwise)
         rc = gemm_pair(ctx, s, g, gu, packed != nullptr, at<uint32_t>(ws, p.n_items_hot), tile_mode, "layer gate_up");
     }
+    // x32: hp's slot-scaled fp16 cast (src/qwen.c:858-877), routed and shared rows
+    if (rc == RMDA_OK && x32) {
+        rc = hip_check(ctx,
+                       rmda_launch_hp_cast(s, at<float>(ws, p.ye), hp, hslot, at<uint32_t>(ws, p.off),
+                                           at<uint32_t>(ws, p.count), E, I, p.sh_row0, p.sh_rows),
+                       "layer hp cast");
+    }
     if (rc == RMDA_OK) {
         rc = prof_mark(ctx, RMDA_STAGE_GATE_UP + 1);
     }
@@ -1134,6 +1244,11 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.mode = RMDA_GEMM_F16;
         g.a = hp;
         g.rowtok = nullptr;
+        g.xscale = nullptr;
+        g.hp32 = nullptr;
+        g.hp_amax = nullptr;
+        g.yscale = hslot;
+        g.ye32 = x32 ? at<float>(ws, p.ye) : nullptr;  // fp32 expert rows (the reference's ye)
         g.lda = I;
         g.w = w_dn;
         g.w_shared = w_sdn;
@@ -1165,7 +1280,20 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     }
     // A8/A9 combine (+ sigmoid-gated shared expert, + hyper-connection streams)
     const rmda_hc_t hcp{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
-    if (rc == RMDA_OK && !(fold_combine && tile_mode == 1u)) {
+    if (rc == RMDA_OK && x32) {
+        // fp32 expert rows: the reference's combine arithmetic
+        // (shader/moe_combine.comp:26-40), fp16 out and/or the streams
+        const float *ye32 = at<float>(ws, p.ye);
+        const rmda_pc_moe_combine_t pm{T, d, K, p.ps, E, args->inj_stride, args->inj_off, args->h != nullptr ? args->hc : 0u};
+        rc = hip_check(ctx,
+                       rmda_launch_combine(s, &pm, wt, slot, ye32, proj,
+                                           shape->shared > 0 ? ye32 + (size_t)p.sh_row0 * d : nullptr, args->inj,
+                                           args->h, args->out),
+                       "layer combine");
+        if (rc == RMDA_OK) {
+            rc = prof_mark(ctx, RMDA_STAGE_COMBINE + 1);
+        }
+    } else if (rc == RMDA_OK && !(fold_combine && tile_mode == 1u)) {
         rc = hip_check(ctx,
                        rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.sh_row0, shape->shared > 0, args->out,
                                              T, d, K, &hcp, fold_combine ? at<uint32_t>(ws, p.n_items_hot) : nullptr),
@@ -1201,7 +1329,7 @@ int rmda_moe_layer_static(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
     if (!check_shape(shape, why, sizeof(why))) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_layer_static: %s", why);
     }
-    const size_t need = plan_layer(shape).total;
+    const size_t need = plan_layer(shape, args->x32 != nullptr).total;
     if (need > RMDA_STATIC_WS_BYTES) {
         return fail(ctx, RMDA_ERR_CAPACITY, "rmda_moe_layer_static: this shape needs %zu bytes of workspace, "
                     "beyond the static scratch's %zu (RMDA_STATIC_WS_BYTES); use rmda_moe_layer with a workspace",

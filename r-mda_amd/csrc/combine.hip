@@ -111,12 +111,13 @@ __global__ __launch_bounds__(256) void combine32_kernel(rmda_pc_moe_combine_t pc
             acc.z += s_sg * v.z;
             acc.w += s_sg * v.w;
         }
-        if (!HC) {
+        if (out != nullptr) {
             uint2 o;
             o.x = (uint32_t)rmda_f2h(acc.x) | ((uint32_t)rmda_f2h(acc.y) << 16);
             o.y = (uint32_t)rmda_f2h(acc.z) | ((uint32_t)rmda_f2h(acc.w) << 16);
             reinterpret_cast<uint2 *>(out + (size_t)r * pc.d)[c] = o;
-        } else {
+        }
+        if (HC) {
             for (uint32_t st = 0; st < pc.hc; st += 1) {
                 float4 *hp = reinterpret_cast<float4 *>(h + ((size_t)r * pc.hc + st) * pc.d) + c;
                 const float g = s_g[st];
@@ -206,9 +207,11 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
     const auto al = [](const void *q, uintptr_t a) { return (reinterpret_cast<uintptr_t>(q) & (a - 1)) == 0; };
     const bool vec_ok = al(y, 16) && al(sh, 16) && al(h, 16) && al(out, 8);
     if (pc->d % 4 == 0 && pc->topk <= RMDA_MAX_TOPK && pc->hc <= RMDA_MAX_HC && vec_ok) {
-        if (out != nullptr) {
+        // the streams when h is given, the fp16 output when out is (both
+        // for the fused layer's slot-scaled mode)
+        if (h == nullptr || pc->hc == 0) {
             hipLaunchKernelGGL(combine32_kernel<false>, dim3(pc->rows), dim3(256), 0, s, *pc, wt, slot, y, proj, sh,
-                               inj, h, out);
+                               inj, nullptr, out);
         } else {
             hipLaunchKernelGGL(combine32_kernel<true>, dim3(pc->rows), dim3(256), 0, s, *pc, wt, slot, y, proj, sh,
                                inj, h, out);

@@ -127,6 +127,37 @@ __device__ __forceinline__ uint32_t rmda_wave_red_u32(uint32_t v) {
     return v;
 }
 
+// The reference's fp16 slot scale (shader/cast_f16.comp): a value cast with
+// slot word amax is multiplied by 2^(141 - biased exponent of amax), or by 1
+// when the slot word is zero, not finite or absent.  rmda_slot_inv is the
+// factor that undoes it (a power of two, so exact for normal results), 1 for
+// amax == NULL: the fused layer's epilogues multiply by it always, which
+// leaves the unscaled path's bits unchanged.
+// The slot word is read through the scalar cache (a constant-address-space
+// load, counted by lgkmcnt), so the GEMM kernels' hand-counted vmcnt waits
+// see nothing but their stage loads.
+__device__ __forceinline__ float rmda_slot_inv(const uint32_t *amax) {
+    if (amax == nullptr) {
+        return 1.0f;
+    }
+    const uint32_t u = *(const __attribute__((address_space(4))) uint32_t *)amax;
+    const float a = __builtin_bit_cast(float, u);
+    if (!(a > 0.0f) || __builtin_isinf(a)) {
+        return 1.0f;
+    }
+    return ldexpf(1.0f, (int)((u >> 23) & 0xffu) - 141);
+}
+
+// A wave's largest |v| into *amax (absmax.comp's atomicMax on the float bits
+// of non-negative values; each lane passes fmaxf over its values, so NaN is
+// skipped as absmax_kernel skips it).  The whole wave must be active.
+__device__ __forceinline__ void rmda_wave_amax(uint32_t *amax, float m) {
+    const uint32_t r = rmda_wave_red_u32<true>(__builtin_bit_cast(uint32_t, m));
+    if (threadIdx.x % RMDA_WAVE == 0) {
+        atomicMax(amax, r);
+    }
+}
+
 // Top-k of one row of logits by one wave (shader/moe_route.comp:20-61),
 // as rmda_route_row = rmda_route_load (the row into registers) then
 // rmda_route_select (the rounds):
@@ -255,10 +286,13 @@ uint32_t rmda_route_fuse_max_cols();
 // hipGetLastError() after the launch.
 
 // router.hip
+// xscale (or NULL): the slot word x16 was cast with; each logit's chunk sum
+// is multiplied by rmda_slot_inv(xscale) before the bias is added (packed or
+// HF-layout tiles for d % 128 == 0 only).
 hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
                               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
-                              const rmda_route_fuse_t *fuse);
+                              const rmda_route_fuse_t *fuse, const uint32_t *xscale = nullptr);
 // Packed router weights: [d/16][rmda_router_cpad(cols)][4][4] fp32, element
 // (k, c) at ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4.
 uint32_t rmda_router_cpad(uint32_t cols);
@@ -290,7 +324,8 @@ struct rmda_rank_args_t {
     uint32_t *count;    // [experts] out, or NULL
     uint32_t *off;      // [experts] out, or NULL
     const uint32_t *off_in; // [experts] caller's offsets (then tile is unused), or NULL
-    uint32_t *done;     // one word, zero on entry, left zero
+    uint32_t *done;     // one word, zero on entry; left zero, except by a routed
+                        // launch (route_proj), which leaves its grid size there
     // work list (optional)
     uint32_t *items;    // uint4 per item {expert, row0, rows, 0}
     uint32_t *n_items;  // one word
@@ -328,10 +363,12 @@ struct rmda_rank_args_t {
     uint32_t fc_shared;
     uint16_t *fc_zero_out;
     uint32_t fc_d;
-    // top-k folded in (optional; npairs <= RMDA_RANK_BLOCK, done zero on
-    // entry): one block per 8 rows routes route_rows rows of logits
-    // (route_proj, row stride route_stride) as route_kernel does, into
-    // route_idx (which must be idx) and route_wt; the last of them ranks
+    // top-k folded in (optional; done zero on entry; npairs <= RMDA_RANK_BLOCK,
+    // or count_all with slot set and 16-byte aligned idx): one block per 8
+    // rows routes route_rows rows of logits (route_proj, row stride
+    // route_stride) as route_kernel does, into route_idx (which must be idx)
+    // and route_wt; the last ceil(npairs / RMDA_RANK_BLOCK) of them to finish
+    // rank
     const float *route_proj;
     uint32_t route_rows;
     uint32_t route_stride;
@@ -432,6 +469,18 @@ struct rmda_gemm_args_t {
     const uint32_t *amax;
     uint32_t sa, sb;
     rmda_fc_t fc;             // F16 mode: the folded-in combine (fc.cnt == NULL: none)
+    // The fused layer's slot-scaled mode (fp32 activations; all NULL
+    // otherwise).  SWIGLU: g and u are multiplied by rmda_slot_inv(xscale)
+    // before SiLU, and with hp32 set the SwiGLU output goes to hp32 as fp32
+    // (same blocked index as the fp16 hp) with its absmax into *hp_amax
+    // instead of fp16 to out.  F16: the output is multiplied by
+    // rmda_slot_inv(yscale), and with ye32 set it is stored to ye32 as fp32
+    // instead of fp16 to out.
+    const uint32_t *xscale;
+    float *hp32;
+    uint32_t *hp_amax;
+    const uint32_t *yscale;
+    float *ye32;
 };
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 // gemm_ref.hip: the F32 (reference matmul_f16_moe) contract on the
@@ -529,3 +578,21 @@ hipError_t rmda_launch_cast(hipStream_t s, const rmda_pc_cast_t *pc, const float
 hipError_t rmda_launch_bf16(hipStream_t s, uint32_t n, uint32_t *w);
 hipError_t rmda_launch_fill_normal(hipStream_t s, void *dst, size_t n, int f16, uint64_t stream,
                                    uint64_t seed, float std);
+// The fused layer's fp32-activation input, in two launches (the reference's
+// absmax.comp + cast_f16.comp with a fresh slot, src/qwen.c:517-539, with no
+// zero-filled slot word needed beforehand): part[b] = the absmax bits of
+// block b's share of x (nparts blocks), then every block folds the parts,
+// casts its share of x with the slot scale into x16, and block 0 stores the
+// absmax to *x_slot and zero to *zero_slot.  n % 4 == 0, x and x16 16-byte
+// aligned.
+#define RMDA_XCAST_PARTS 256u
+hipError_t rmda_launch_x_absmax(hipStream_t s, const float *x, size_t n, uint32_t *part);
+hipError_t rmda_launch_x_cast(hipStream_t s, const float *x, size_t n, const uint32_t *part, uint16_t *x16,
+                              uint32_t *x_slot, uint32_t *zero_slot);
+// hp16[i] = fp16(hp32[i] * scale(*slot)) over the blocked hp of the slot-scaled
+// mode, for the routed rows [0, off[E-1] + count[E-1] rounded up to 16) and,
+// when sh_rows > 0, the shared expert's rows [sh_row0, sh_row0 + sh_rows
+// rounded up to 16); inter % 4 == 0.
+hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *slot,
+                               const uint32_t *off, const uint32_t *count, uint32_t experts, uint32_t inter,
+                               uint32_t sh_row0, uint32_t sh_rows);

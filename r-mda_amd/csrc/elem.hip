@@ -459,3 +459,121 @@ hipError_t rmda_launch_fill_normal(hipStream_t s, void *dst, size_t n, int f16, 
                        seed, std);
     return hipGetLastError();
 }
+
+// ---- the fused layer's fp32-activation (slot-scaled) mode ----
+
+namespace {
+
+// float bits of the largest fabsf over the values a thread saw, per block
+__device__ __forceinline__ uint32_t block_max_bits(float m) {
+    __shared__ float red[256];
+    const uint32_t tid = threadIdx.x;
+    red[tid] = m;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (tid < s) {
+            red[tid] = fmaxf(red[tid], red[tid + s]);
+        }
+        __syncthreads();
+    }
+    return __builtin_bit_cast(uint32_t, red[0]);
+}
+
+// the cast_f16.comp scale of an absmax value (cast_scale without the slot)
+__device__ __forceinline__ float amax_scale(uint32_t u) {
+    const float a = __builtin_bit_cast(float, u);
+    if (!(a > 0.0f) || __builtin_isinf(a)) {
+        return 1.0f;
+    }
+    return ldexpf(1.0f, 141 - (int)((u >> 23) & 0xffu));
+}
+
+__device__ __forceinline__ uint2 cast4(const float4 &v, float sc) {
+    return make_uint2((uint32_t)rmda_f2h(v.x * sc) | ((uint32_t)rmda_f2h(v.y * sc) << 16),
+                      (uint32_t)rmda_f2h(v.z * sc) | ((uint32_t)rmda_f2h(v.w * sc) << 16));
+}
+
+// absmax.comp over x, one part per block (no slot word to clear first)
+__global__ __launch_bounds__(256) void x_absmax_kernel(const float4 *__restrict__ x, size_t n4,
+                                                       uint32_t *__restrict__ part) {
+    float m = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 v = x[i];
+        m = fmaxf(m, fabsf(v.x));
+        m = fmaxf(m, fabsf(v.y));
+        m = fmaxf(m, fabsf(v.z));
+        m = fmaxf(m, fabsf(v.w));
+    }
+    const uint32_t r = block_max_bits(m);
+    if (threadIdx.x == 0) {
+        part[blockIdx.x] = r;
+    }
+}
+
+// every block folds the parts (the values are non-negative, so their bit
+// patterns order as the values do), then cast_f16.comp over its share
+__global__ __launch_bounds__(256) void x_cast_kernel(const float4 *__restrict__ x, size_t n4,
+                                                     const uint32_t *__restrict__ part, uint2 *__restrict__ x16,
+                                                     uint32_t *__restrict__ x_slot, uint32_t *__restrict__ zero_slot) {
+    __shared__ uint32_t s_amax;
+    if (threadIdx.x < RMDA_WAVE) {
+        uint32_t m = 0;
+        for (uint32_t i = threadIdx.x; i < RMDA_XCAST_PARTS; i += RMDA_WAVE) {
+            m = max(m, part[i]);
+        }
+        m = rmda_wave_red_u32<true>(m);
+        if (threadIdx.x == 0) {
+            s_amax = m;
+        }
+    }
+    __syncthreads();
+    const uint32_t amax = s_amax;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *x_slot = amax;
+        *zero_slot = 0u;
+    }
+    const float sc = amax_scale(amax);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        x16[i] = cast4(x[i], sc);
+    }
+}
+
+// the blocked hp: 16-row groups are contiguous runs of 16 * inter values
+__global__ __launch_bounds__(256) void hp_cast_kernel(const float4 *__restrict__ hp32, uint2 *__restrict__ hp16,
+                                                      const uint32_t *__restrict__ slot,
+                                                      const uint32_t *__restrict__ off,
+                                                      const uint32_t *__restrict__ count, uint32_t experts,
+                                                      uint32_t inter, uint32_t sh_row0, uint32_t sh_rows) {
+    const uint32_t routed_end = off[experts - 1] + (count[experts - 1] + 15u) / 16u * 16u;
+    const size_t n_r = (size_t)routed_end * inter / 4;
+    const size_t s0 = (size_t)sh_row0 * inter / 4;
+    const size_t n_s = (size_t)((sh_rows + 15u) / 16u * 16u) * inter / 4;
+    const float sc = amax_scale(*slot);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_r + n_s; i += (size_t)gridDim.x * 256) {
+        const size_t j = i < n_r ? i : s0 + (i - n_r);
+        hp16[j] = cast4(hp32[j], sc);
+    }
+}
+
+}  // namespace
+
+hipError_t rmda_launch_x_absmax(hipStream_t s, const float *x, size_t n, uint32_t *part) {
+    hipLaunchKernelGGL(x_absmax_kernel, dim3(RMDA_XCAST_PARTS), dim3(256), 0, s,
+                       reinterpret_cast<const float4 *>(x), n / 4, part);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_x_cast(hipStream_t s, const float *x, size_t n, const uint32_t *part, uint16_t *x16,
+                              uint32_t *x_slot, uint32_t *zero_slot) {
+    hipLaunchKernelGGL(x_cast_kernel, dim3(RMDA_XCAST_PARTS), dim3(256), 0, s, reinterpret_cast<const float4 *>(x),
+                       n / 4, part, reinterpret_cast<uint2 *>(x16), x_slot, zero_slot);
+    return hipGetLastError();
+}
+
+hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *slot,
+                               const uint32_t *off, const uint32_t *count, uint32_t experts, uint32_t inter,
+                               uint32_t sh_row0, uint32_t sh_rows) {
+    hipLaunchKernelGGL(hp_cast_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float4 *>(hp32),
+                       reinterpret_cast<uint2 *>(hp16), slot, off, count, experts, inter, sh_row0, sh_rows);
+    return hipGetLastError();
+}

@@ -95,7 +95,7 @@ __device__ __forceinline__ uint32_t slab_row(uint32_t slab, uint32_t n, uint32_t
 // the stores of a finished tile are never counted in a wait's allowance, so
 // each wait is exact or conservative.
 
-template <int MODE, int BN, int BK, int STAGES, bool PACKED, int BPOL>
+template <int MODE, int BN, int BK, int STAGES, bool PACKED, int BPOL, bool SC = false>
 __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t MB = BM / 64;             // row blocks
     constexpr uint32_t NB = BN / 64;             // column blocks
@@ -125,6 +125,9 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
 
     // ---- this workgroup's tasks (task_sched_t) ----
     const_u32p items = (const_u32p)g.items;
+    // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
+    const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
+    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
 #pragma unroll
                             for (int j = 0; j < 4; j += 1) {
                                 const uint32_t col = c_nt * BN + wn * 64 + j * 16 + fr;
-                                O[(size_t)(c_row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
+                                down_store<SC>(g, O, (size_t)(c_row0 + rr) * g.ldo + col, acc[i][j][v] * yinv);
                             }
                         }
                     }
@@ -343,6 +346,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                 // same output columns
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
                 const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
+                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -351,13 +355,16 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                         if (rr < c_rows) {
 #pragma unroll
                             for (int j = 0; j < 2; j += 1) {
-                                const float gt = acc[i][j][v];
-                                const float up = acc[i][j + 2][v];
+                                const float gt = acc[i][j][v] * xinv;
+                                const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
                             }
                         }
                     }
+                }
+                if (SC) {
+                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -550,7 +557,7 @@ __device__ __forceinline__ task_desc_t task_desc(const task_sched_t &sched, cons
 // their ye tile with device-scope stores, wait for them, take one from the
 // arrival counter of each stored row's (token, 64 columns), and the wave that
 // takes a counter's last one sums that token's rows for its 64 columns.
-template <int MODE, int STAGES, int BPOL, int NDW, bool DB, bool FC = false>
+template <int MODE, int STAGES, int BPOL, int NDW, bool DB, bool FC = false, bool SC = false>
 __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t BN = 256;
     constexpr uint32_t BK = 32;
@@ -580,6 +587,9 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
 
     // ---- this workgroup's tasks (task_sched_t) ----
     const_u32p items = (const_u32p)g.items;
+    // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
+    const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
+    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
@@ -789,10 +799,10 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                                 if (FC) {
                                     // through to the device coherence point: the
                                     // token's combine may run on another XCD
-                                    __hip_atomic_store(dst, rmda_f2h(acc[i][j][v]), __ATOMIC_RELAXED,
+                                    __hip_atomic_store(dst, rmda_f2h(acc[i][j][v] * yinv), __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
                                 } else {
-                                    *dst = rmda_f2h(acc[i][j][v]);
+                                    down_store<SC>(g, O, (size_t)(c_row0 + rr) * g.ldo + col, acc[i][j][v] * yinv);
                                 }
                             }
                         }
@@ -805,6 +815,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             } else {
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
                 const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
+                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -813,13 +824,16 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                         if (rr < c_rows) {
 #pragma unroll
                             for (int j = 0; j < 2; j += 1) {
-                                const float gt = acc[i][j][v];
-                                const float up = acc[i][j + 2][v];
+                                const float gt = acc[i][j][v] * xinv;
+                                const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
                             }
                         }
                     }
+                }
+                if (SC) {
+                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -846,7 +860,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
 //     activation row is 128 bytes; chunk c of row r sits at c ^ ((r>>1)&7),
 //     so each 16-lane fragment read touches 16 distinct bank groups.
 // Needs k % 64 == 0 (pairs never straddle a task).
-template <int STAGES, int BPOL, int NDW>
+template <int STAGES, int BPOL, int NDW, bool SC = false>
 __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t BN = 256;
     constexpr uint32_t BK = 32;
@@ -880,6 +894,8 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
 
     const_u32p items = (const_u32p)g.items;
+    // the slot-scaled mode's inverse scale (1 otherwise, which changes no bits)
+    const float xinv = SC ? rmda_slot_inv(g.xscale) : 1.0f;
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
@@ -1086,6 +1102,7 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
             uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
             const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
             const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
+            float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
             for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -1094,13 +1111,16 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
                     if (rr < c_rows) {
 #pragma unroll
                         for (int j = 0; j < 2; j += 1) {
-                            const float gt = acc[i][j][v];
-                            const float up = acc[i][j + 2][v];
+                            const float gt = acc[i][j][v] * xinv;
+                            const float up = acc[i][j + 2][v] * xinv;
                             const float h = rmda_swiglu_fast(gt, up);
-                            O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
+                            swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
                         }
                     }
                 }
+            }
+            if (SC) {
+                rmda_wave_amax(g.hp_amax, hmax);
             }
         }
         ks += 1;
@@ -1149,12 +1169,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t *__restrict__ 
     }
 }
 
-template <int MODE, int BN, int BK, int STAGES, int BPOL>
+template <int MODE, int BN, int BK, int STAGES, int BPOL, bool SC = false>
 hipError_t launch_cfg(hipStream_t s, const rmda_gemm_args_t *a, dim3 grid, bool packed) {
     if (packed) {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true, BPOL>), grid, dim3(BM / 64 * BN), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, true, BPOL, SC>), grid, dim3(BM / 64 * BN), 0, s, *a);
     } else {
-        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false, BPOL>), grid, dim3(BM / 64 * BN), 0, s, *a);
+        hipLaunchKernelGGL((gemm2_kernel<MODE, BN, BK, STAGES, false, BPOL, SC>), grid, dim3(BM / 64 * BN), 0, s, *a);
     }
     return hipGetLastError();
 }
@@ -1167,6 +1187,31 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     // persistent: one workgroup per CU, a multiple of the 8 XCDs
     const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
     const dim3 grid(wgs);
+    // the slot-scaled mode (fp32 SwiGLU output or fp32 rows) has its own
+    // instantiations, of the default configurations only
+    const bool sc = a->hp32 != nullptr || a->ye32 != nullptr;
+    if (sc) {
+        if ((MODE == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) || (MODE == RMDA_GEMM_F16) != (a->ye32 != nullptr) ||
+            a->fc.cnt != nullptr) {
+            return hipErrorInvalidValue;
+        }
+        if (c.spec == 0 || !packed) {
+            if (c.stages != 5 || c.bpol != 2) {
+                return hipErrorInvalidValue;
+            }
+            return launch_cfg<MODE, 256, 32, 5, 2, true>(s, a, grid, packed);
+        }
+        if (c.spec == 7 && MODE == RMDA_GEMM_SWIGLU && a->k % 64 == 0) {
+            hipLaunchKernelGGL((gemm4_kernel<5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
+        } else if (c.spec == 5 || ((c.spec == 6 || c.spec == 7) && MODE == RMDA_GEMM_SWIGLU)) {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true, false, true>), grid, dim3(16 * RMDA_WAVE), 0, s,
+                               *a);
+        } else {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false, false, true>), grid, dim3(16 * RMDA_WAVE), 0, s,
+                               *a);
+        }
+        return hipGetLastError();
+    }
     if (c.spec != 0 && packed) {
         if (c.spec == 7 && MODE == RMDA_GEMM_SWIGLU && a->k % 64 == 0) {
             hipLaunchKernelGGL((gemm4_kernel<5, 2, 4>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);

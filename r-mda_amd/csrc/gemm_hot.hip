@@ -41,7 +41,7 @@ constexpr uint32_t HN = 256;               // N tile = one packed slab
 constexpr uint32_t HK = 32;                // K step
 constexpr uint32_t NW = 8;                 // waves
 
-template <int MODE, int STAGES, typename SCHED, bool PP, int BPOL>
+template <int MODE, int STAGES, typename SCHED, bool PP, int BPOL, bool SC = false>
 __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t CH = HK / 8;                  // 16-byte chunks per row
     constexpr uint32_t RPI = 64 / CH;                // rows per DMA instruction
@@ -63,6 +63,9 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     const uint32_t wn = w % 4;
 
     const_u32p items = (const_u32p)g.items;
+    // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
+    const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
+    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
     const uint32_t ntiles = g.n_w / HN;
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
     const SCHED sched(n_items, ntiles);
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
 #pragma unroll
                             for (int j = 0; j < 4; j += 1) {
                                 const uint32_t col = c_nt * HN + wn * 64 + j * 16 + fr;
-                                O[(size_t)(c_row0 + rr) * g.ldo + col] = rmda_f2h(acc[i][j][v]);
+                                down_store<SC>(g, O, (size_t)(c_row0 + rr) * g.ldo + col, acc[i][j][v] * yinv);
                             }
                         }
                     }
@@ -224,6 +227,7 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
                 // slab rows wn*64 .. +64 are 32 gate rows then the 32 matching
                 // up rows: blocks j (gate) and j + 2 (up) share output columns
                 const uint32_t colbase = c_nt * (HN / 2) + wn * 32;
+                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 8; i += 1) {
 #pragma unroll
@@ -232,13 +236,16 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
                         if (rr < c_rows) {
 #pragma unroll
                             for (int j = 0; j < 2; j += 1) {
-                                const float gt = acc[i][j][v];
-                                const float up = acc[i][j + 2][v];
+                                const float gt = acc[i][j][v] * xinv;
+                                const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                O[rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo)] = rmda_f2h(h);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
                             }
                         }
                     }
+                }
+                if (SC) {
+                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -359,6 +366,21 @@ hipError_t rmda_launch_gemm_hot(hipStream_t s, const rmda_gemm_args_t *a, uint32
         return hipSuccess;
     }
     const dim3 gr(grid >= 8 ? grid / 8 * 8 : 8);  // persistent: one workgroup per CU, whole XCDs
+    if (a->hp32 != nullptr || a->ye32 != nullptr) {
+        // the slot-scaled mode: the default configuration only
+        if ((a->mode == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) || (a->mode == RMDA_GEMM_F16) != (a->ye32 != nullptr) ||
+            stages != 4 || sched != 0) {
+            return hipErrorInvalidValue;
+        }
+        if (a->mode == RMDA_GEMM_SWIGLU) {
+            hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_SWIGLU, 4, task_sched_t, true, 0, true>), gr,
+                               dim3(NW * RMDA_WAVE), 0, s, *a);
+        } else {
+            hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_F16, 4, task_sched_t, true, 0, true>), gr,
+                               dim3(NW * RMDA_WAVE), 0, s, *a);
+        }
+        return hipGetLastError();
+    }
     if (a->mode == RMDA_GEMM_SWIGLU) {
         launch_mode<RMDA_GEMM_SWIGLU>(s, a, gr, stages, sched);
     } else {

@@ -127,4 +127,31 @@ struct chunk_sched_t {
 
 typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
 
+// One SwiGLU output of the gate_up epilogue: fp16 into hp, or in the
+// slot-scaled mode (SC, a template parameter of every GEMM kernel, so the
+// default epilogue carries no test of it) fp32 into hp32 with its magnitude
+// into the lane's running maximum (rmda_wave_amax merges it after the tile).
+// Both tiles store through this, so they stay bitwise equal in either mode.
+template <bool SC>
+__device__ __forceinline__ void swiglu_store(const rmda_gemm_args_t &g, uint16_t *O, size_t hi, float h,
+                                             float &hmax) {
+    if constexpr (SC) {
+        g.hp32[hi] = h;
+        hmax = fmaxf(hmax, fabsf(h));
+    } else {
+        O[hi] = rmda_f2h(h);
+    }
+}
+
+// One output of the down epilogue, already multiplied by the inverse hp
+// slot scale: fp16 into ye, or fp32 into ye32 in the slot-scaled mode.
+template <bool SC>
+__device__ __forceinline__ void down_store(const rmda_gemm_args_t &g, uint16_t *O, size_t i, float y) {
+    if constexpr (SC) {
+        g.ye32[i] = y;
+    } else {
+        O[i] = rmda_f2h(y);
+    }
+}
+
 }  // namespace rmda_gemm

@@ -218,7 +218,8 @@ template <bool W_PACKED, bool FUSE, int TT, int TPW>
 __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     const uint16_t *__restrict__ x16, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t cpad, uint32_t stride,
-    uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, rmda_route_fuse_t fz, uint32_t col0) {
+    uint32_t nbias, uint32_t *zero_words, uint32_t n_zero, rmda_route_fuse_t fz, uint32_t col0,
+    const uint32_t *xscale) {
     constexpr uint32_t NCOL = 16 * TPW;
     constexpr int KS = MF_KS;
     constexpr uint32_t NW = MF_NW;
@@ -246,6 +247,7 @@ __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
     const uint32_t nsub = L / KS;  // d % (8*KS) == 0 is a launch condition
     const uint32_t t0 = blockIdx.x * TOK;
     const uint32_t c0 = col0 + blockIdx.y * NCOL;  // columns from col0 (the wide tile's remainder)
+    const float xinv = rmda_slot_inv(xscale);     // 1 unless x16 was cast with a slot
     const uint32_t kk = lane / 16;
     const uint32_t ln = lane % 16;  // A: token row; B: column within a tile
 
@@ -417,6 +419,7 @@ __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
         for (int qq = 1; qq < NQ; qq += 1) {
             v = v + red[qq][t][l];
         }
+        v = v * xinv;
         if (bias != nullptr && cc < nbias) {
             v = v + bias[cc];
         }
@@ -475,7 +478,8 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
                                                             const float *__restrict__ bias,
                                                             float *__restrict__ proj, uint32_t rows, uint32_t d,
                                                             uint32_t cols, uint32_t cpad, uint32_t stride,
-                                                            uint32_t nbias, uint32_t *zero_words, uint32_t n_zero) {
+                                                            uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
+                                                            const uint32_t *xscale) {
     __shared__ float4 xs[2][NQ][RW_TT][RMDA_WAVE];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
@@ -610,6 +614,7 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
     // D[4*kk + v][lane % 16] of token tile tt is token 16*tt + 4*kk + v
     const bool cok = c < cols;
     const float bv = bias != nullptr && c < nbias ? bias[c] : 0.0f;
+    const float xinv = rmda_slot_inv(xscale);
 #pragma unroll
     for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
 #pragma unroll
@@ -619,6 +624,7 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
             for (uint32_t q = 1; q < NQ; q += 1) {
                 sum = sum + acc[tt][q][v];
             }
+            sum = sum * xinv;
             if (bias != nullptr && c < nbias) {
                 sum = sum + bv;
             }
@@ -654,22 +660,23 @@ namespace {
 template <bool FUSE, int TT, int TPW>
 void launch_mf_tile(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
                     const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
-                    uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz, uint32_t col0) {
+                    uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz, uint32_t col0,
+                    const uint32_t *xscale) {
     const dim3 grid((rows + MF_TOK * TT - 1) / (MF_TOK * TT), FUSE ? 1 : (cols - col0 + 16 * TPW - 1) / (16 * TPW));
     const dim3 block(MF_NW * RMDA_WAVE);
     if (w_packed) {
         hipLaunchKernelGGL((router_mf_kernel<true, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
-                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0);
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0, xscale);
     } else {
         hipLaunchKernelGGL((router_mf_kernel<false, FUSE, TT, TPW>), grid, block, 0, s, x16, w, bias, proj, rows, d,
-                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0);
+                           cols, cpad, stride, nbias, zero_words, n_zero, fz, col0, xscale);
     }
 }
 
 template <bool FUSE>
 void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const uint16_t *x16, const float *w,
                const float *bias, float *proj, uint32_t d, uint32_t cpad, uint32_t stride, uint32_t nbias,
-               uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz) {
+               uint32_t *zero_words, uint32_t n_zero, const rmda_route_fuse_t &fz, const uint32_t *xscale) {
     uint32_t col0 = 0;
     if (!FUSE && w_packed) {
         // the wide tile takes whole 128-column blocks when they give the GPU
@@ -679,7 +686,7 @@ void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const
         if (nbw > 0 && (rows + RW_TOK - 1) / RW_TOK * nbw >= RW_MIN_WGS) {
             const dim3 grid((rows + RW_TOK - 1) / RW_TOK, nbw);
             hipLaunchKernelGGL(router_wide_kernel, grid, dim3(RW_NT), 0, s, x16, w, bias, proj, rows, d, cols, cpad,
-                               stride, nbias, zero_words, n_zero);
+                               stride, nbias, zero_words, n_zero, xscale);
             col0 = nbw * RW_COL;
             zero_words = nullptr;
             if (col0 == cols) {
@@ -695,10 +702,10 @@ void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const
                        (!FUSE || cols <= 16u * MF_TPW_SMALL);
     if (small) {
         launch_mf_tile<FUSE, MF_TT_SMALL, MF_TPW_SMALL>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride,
-                                                        nbias, zero_words, n_zero, fz, col0);
+                                                        nbias, zero_words, n_zero, fz, col0, xscale);
     } else {
         launch_mf_tile<FUSE, MF_TT, MF_TPW>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride, nbias,
-                                            zero_words, n_zero, fz, col0);
+                                            zero_words, n_zero, fz, col0, xscale);
     }
 }
 
@@ -707,9 +714,9 @@ void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const
 hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w, int w_packed, const float *bias,
                               float *proj, uint32_t rows, uint32_t d, uint32_t cols, uint32_t stride,
                               uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
-                              const rmda_route_fuse_t *fuse) {
+                              const rmda_route_fuse_t *fuse, const uint32_t *xscale) {
     const bool mf = d % 128 == 0 && rows > 0;
-    if ((w_packed || fuse != nullptr) && !mf) {
+    if ((w_packed || fuse != nullptr || xscale != nullptr) && !mf) {
         return hipErrorInvalidValue;
     }
     if (fuse != nullptr && (fuse->experts > cols || cols > rmda_route_fuse_max_cols())) {
@@ -719,10 +726,10 @@ hipError_t rmda_launch_router(hipStream_t s, const uint16_t *x16, const float *w
         const uint32_t cpad = rmda_router_cpad(cols);
         if (fuse != nullptr) {
             launch_mf<true>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride, nbias, zero_words, n_zero,
-                            *fuse);
+                            *fuse, xscale);
         } else {
             launch_mf<false>(s, rows, cols, w_packed, x16, w, bias, proj, d, cpad, stride, nbias, zero_words, n_zero,
-                             rmda_route_fuse_t{});
+                             rmda_route_fuse_t{}, xscale);
         }
         return hipGetLastError();
     }

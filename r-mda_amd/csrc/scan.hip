@@ -141,8 +141,15 @@ __global__ __launch_bounds__(512) void scan_kernel(const uint32_t *__restrict__ 
     }
 }
 
+// Upper bound on the polls of a rank block that waits for the routing
+// blocks of its launch (each poll is one device-scope load and a short
+// sleep, so about a second in all): a safety net that lets every wave exit
+// even if the ticket never completed; it is never reached in a correct run.
+constexpr uint32_t kRouteWaitPolls = 1u << 20;
+
 // NV > 0: the top-k folded in (rmda_rank_args_t::route_proj), NV logits per
-// lane: one block per NT / 64 rows routes, and the last of them ranks.
+// lane: one block per NT / 64 rows routes; the blocks that take the last
+// nb tickets (nb = the rank blocks of npairs) then rank.
 template <uint32_t NT, int NV>
 __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     __shared__ unsigned long long msk[NT / RMDA_WAVE][RMDA_MAX_EXPERTS];
@@ -160,15 +167,16 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     // top-k slot of most tokens) half of a wave's lanes add to the same
     // expert, and the LDS serialises adds to one word.  A row of CW words
     // (one spare) puts copy s of expert e in its own bank.
-    constexpr uint32_t CS = NT >= 1024 ? 8u : 1u;  // count_all runs 1024-thread blocks
+    constexpr uint32_t CS = NT >= 1024 || NV > 0 ? 8u : 1u;  // the launches that may count_all
     constexpr uint32_t CW = RMDA_MAX_EXPERTS + 1u;
     __shared__ uint32_t hcopy[2 * CS * CW];  // [pre, post][CS][CW]
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t w = tid / RMDA_WAVE;
     const uint32_t E = a.experts;
-    const uint32_t b = NV > 0 ? 0u : blockIdx.x;  // routed: the ranking block stands for the one rank block
-    const uint32_t nb = NV > 0 ? 1u : gridDim.x;
+    // routed: rank blocks are dealt by ticket below; otherwise one per workgroup
+    const uint32_t nb = NV > 0 ? (a.npairs + RMDA_RANK_BLOCK - 1u) / RMDA_RANK_BLOCK : gridDim.x;
+    uint32_t b = NV > 0 ? 0u : blockIdx.x;
     // every block counts every pair itself: no hand-off, and each block
     // writes its own slots (see rmda_rank_args_t::count_all)
     const bool all = a.count_all != 0 && nb > 1;
@@ -185,14 +193,19 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
             hcopy[i] = 0u;
         }
     }
-    // Top-k folded in: block r's wave w routes row 4r + w as route_kernel
-    // does, storing its experts at device scope; the last block to finish
-    // (ticket) then ranks every pair as the single rank block, reading idx at
-    // device scope.  The other blocks leave.  Ordering without a fence: the
-    // device-scope idx stores are written through to the device coherence
-    // point and acknowledged before s_waitcnt vmcnt(0) lets the wave reach
-    // the barrier that precedes the ticket, and the last block's
-    // device-scope loads are issued after its ticket returned.
+    // Top-k folded in: block r's wave w routes row (NT/64)*r + w as
+    // route_kernel does, storing its experts with device-scope stores.  Each
+    // block then takes a ticket (a zero word the router kernel cleared at the
+    // start of the call) with a device-scope release increment, so its idx
+    // stores happen before the ticket.  The blocks that draw the last nb
+    // tickets become rank blocks nb-1 ... 0 in ticket order and wait until
+    // every block has drawn one (the one that drew the last ticket needs no
+    // wait); a device-scope acquire fence then makes every block's idx visible
+    // to this block's loads, and they rank as the nb blocks of an unrouted
+    // launch do.  The other blocks leave.  At most nb blocks ever wait, and a
+    // waiting block drew its ticket after routing, so the blocks still to
+    // route can always be scheduled (the device holds far more than nb of
+    // these workgroups at once): no co-residency of the whole grid is needed.
     if constexpr (NV > 0) {
         const uint32_t t = blockIdx.x * (NT / RMDA_WAVE) + w;
         if (t < a.route_rows) {
@@ -203,15 +216,26 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        const uint32_t G = gridDim.x;
         if (tid == 0) {
-            // the increment wraps the ticket back to 0 on the last block
-            s_last = __builtin_amdgcn_atomic_inc32(a.done, gridDim.x - 1, __ATOMIC_RELAXED, "agent") ==
-                     gridDim.x - 1;
+            const uint32_t tk = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            if (tk + nb >= G) {
+                if (tk + 1u < G) {
+                    for (uint32_t n = 0;
+                         __hip_atomic_load(a.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G && n < kRouteWaitPolls;
+                         n += 1) {
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
+            s_last = tk;
         }
         __syncthreads();
-        if (!s_last) {
+        if (s_last + nb < G) {
             return;
         }
+        b = G - 1u - s_last;
     }
     // a pair's expert: written by other blocks of this launch when it routed
     auto pair_expert = [&](uint32_t pr) -> uint32_t {
@@ -711,13 +735,17 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     // config 5, 20 blocks over 512 experts: rank 15.5 -> 10.2 us; config 3
     // 7.6 -> 7.35 us; one block is 0.15 us slower with 1024)
     if (a->route_proj != nullptr) {
-        // top-k folded in: one block per 8 rows routes, the last one ranks
-        // (8-wave blocks: decode rank 7.45-7.65 -> 7.16-7.19 us against 4-wave
-        // ones; 16-wave ones took 8.8-9.1, their last block then routing
-        // as well as ranking the most)
+        // top-k folded in: one block per 8 rows routes, the last nb to finish
+        // rank (8-wave blocks: decode rank 7.45-7.65 -> 7.16-7.19 us against
+        // 4-wave ones; 16-wave ones took 8.8-9.1, their last block then
+        // routing as well as ranking the most).  Several rank blocks need
+        // count_all (each counts every pair, so none waits for another's
+        // totals) and write the permutation themselves.
         constexpr uint32_t NTR = 512;
-        if (nb != 1 || a->experts > RMDA_MAX_EXPERTS || a->topk == 0 || a->done == nullptr ||
-            a->route_rows * a->topk != a->npairs) {
+        const bool multi_ok = a->count_all != 0 && a->slot != nullptr && a->npairs <= RMDA_RANK_ALL_MAX &&
+                              (reinterpret_cast<uintptr_t>(a->idx) & 15u) == 0;
+        if ((nb != 1 && !multi_ok) || a->experts > RMDA_MAX_EXPERTS || a->topk == 0 || a->done == nullptr ||
+            a->route_idx != a->idx || (uint64_t)a->route_rows * a->topk != a->npairs) {
             return hipErrorInvalidValue;
         }
         const uint32_t nv = (a->experts + RMDA_WAVE - 1) / RMDA_WAVE;

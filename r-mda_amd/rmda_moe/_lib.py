@@ -79,7 +79,7 @@ class LayerArgs(ctypes.Structure):
     _fields_ = [("x", _p), ("w_router", _p), ("bias", _p), ("w_gate_up", _p), ("w_down", _p),
                 ("w_sh_gate_up", _p), ("w_sh_down", _p), ("out", _p), ("workspace", _p),
                 ("workspace_bytes", ctypes.c_size_t), ("packed", _p), ("h", _p), ("inj", _p),
-                ("inj_stride", _u32), ("inj_off", _u32), ("hc", _u32)]
+                ("inj_stride", _u32), ("inj_off", _u32), ("hc", _u32), ("x32", _p)]
 
 
 ST_BF16, ST_F16, ST_F32, ST_I64, ST_I32, ST_U8, ST_OTHER = 0, 1, 2, 3, 4, 5, 15
@@ -120,11 +120,13 @@ SIGNATURES = {
     "rmda_moe_set_hot_rows": (ctypes.c_int, [_p, _u32]),
     "rmda_moe_set_tile_policy": (ctypes.c_int, [_p, ctypes.c_int]),
     "rmda_moe_set_fused_combine": (ctypes.c_int, [_p, ctypes.c_int]),
+    "rmda_moe_set_route_in_rank": (ctypes.c_int, [_p, ctypes.c_int]),
     "rmda_moe_ctx_error": (ctypes.c_int, [_p]),
     "rmda_moe_ctx_message": (ctypes.c_char_p, [_p]),
     "rmda_moe_ctx_clear_error": (None, [_p]),
     "rmda_moe_sync": (ctypes.c_int, [_p]),
     "rmda_moe_version": (ctypes.c_char_p, []),
+    "rmda_moe_abi_version": (ctypes.c_int, []),
     "rmda_moe_route": (ctypes.c_int, [_p, _p, _p, _p, _p, _p]),
     "rmda_moe_scan": (ctypes.c_int, [_p, _p, _p, _p, _p, _u32]),
     "rmda_moe_scatter": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p]),
@@ -138,6 +140,7 @@ SIGNATURES = {
     "rmda_qwen_bf16": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_router": (ctypes.c_int, [_p, _p, _p, _p, _p, _p]),
     "rmda_moe_workspace_bytes": (ctypes.c_size_t, [_p]),
+    "rmda_moe_workspace_bytes_x32": (ctypes.c_size_t, [_p]),
     "rmda_moe_workspace_layout": (ctypes.c_int, [_p, _p]),
     "rmda_moe_layer": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_packed_bytes": (ctypes.c_size_t, [_p]),

@@ -49,6 +49,12 @@ def workspace_bytes(shape):
     return _lib.lib().rmda_moe_workspace_bytes(ctypes.byref(s))
 
 
+def workspace_bytes_x32(shape):
+    """rmda_moe_workspace_bytes_x32 (the fp32-activation mode); 0 = rejected."""
+    s = shape_struct(shape)
+    return _lib.lib().rmda_moe_workspace_bytes_x32(ctypes.byref(s))
+
+
 def packed_bytes(shape):
     """rmda_moe_packed_bytes; 0 means the shape is rejected.  Host-only."""
     s = shape_struct(shape)
@@ -110,6 +116,11 @@ class Context:
     def set_tile_policy(self, policy):
         """rmda_moe_set_tile_policy (TILE_ADAPTIVE, TILE_AUTO, TILE_STREAM, TILE_HOT)."""
         self._check(self.L.rmda_moe_set_tile_policy(self.h, int(policy)))
+
+    def set_route_in_rank(self, on):
+        """rmda_moe_set_route_in_rank: the top-k inside the rank launch above
+        one rank block (two launches before gate_up instead of three)."""
+        self._check(self.L.rmda_moe_set_route_in_rank(self.h, 1 if on else 0))
 
     def set_fused_combine(self, on):
         """rmda_moe_set_fused_combine: fold the combine into the down GEMM."""
@@ -192,14 +203,15 @@ class Context:
     # ---- fused layer ----
 
     def layer(self, shape, x, w_router, bias, w_gate_up, w_down, w_sh_gate_up, w_sh_down, out, workspace,
-              packed=None, h=None, inj=None, inj_stride=0, inj_off=0, hc=0):
+              packed=None, h=None, inj=None, inj_stride=0, inj_off=0, hc=0, x32=None):
         """rmda_moe_layer; with `h` (rows x hc x d fp32) the output is injected into
-        the hyper-connection streams (and `out` may be None)."""
+        the hyper-connection streams (and `out` may be None); with `x32` (fp32
+        activations, x then None) the reference's scale-slot protocol runs."""
         s = shape_struct(shape)
         args = LayerArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(w_gate_up), _ptr(w_down),
                          _ptr(w_sh_gate_up), _ptr(w_sh_down), _ptr(out), _ptr(workspace),
                          workspace.numel() * workspace.element_size(), _ptr(packed), _ptr(h), _ptr(inj),
-                         inj_stride, inj_off, hc)
+                         inj_stride, inj_off, hc, _ptr(x32))
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
 
     def layer_static(self, shape, x, w_router, bias, out, packed=None, w_gate_up=None, w_down=None,

@@ -46,6 +46,9 @@ def test_struct_layouts_match_reference_push_constants():
 
 def test_version_and_stage_names(L):
     assert b"gfx950" in L.rmda_moe_version()
+    # the library was built against this header's binary interface
+    want = int(re.search(r"#define RMDA_MOE_ABI_VERSION (\d+)", open(_lib.HEADER_PATH).read()).group(1))
+    assert L.rmda_moe_abi_version() == want
     names = [L.rmda_moe_prof_stage_name(i).decode() for i in range(_lib.PROF_STAGES)]
     assert names == ["router", "route", "rank", "permute", "gate_up", "down", "combine"]
     assert L.rmda_moe_prof_stage_name(_lib.PROF_STAGES) is None

@@ -365,31 +365,54 @@ def test_elem_absmax_cast_bf16_closed_forms():
 
 # ---------------------------------------------------------------- whole layer
 
-def np_layer(host, res, hp_fp16=True):
+def slot_round(v):
+    """numpy restatement of absmax.comp + cast_f16.comp and the consuming
+    GEMM's division: v * 2^(141 - biased exponent(max|v|)) rounded to fp16
+    (numpy's RNE), then divided by the same power of two, in float64."""
+    v32 = np.asarray(v, np.float32)
+    amax = np.float32(np.abs(v32).max())
+    if not (amax > 0) or not np.isfinite(amax):
+        return v32.astype(np.float16).astype(np.float64)
+    e = int((amax.view(np.uint32) >> np.uint32(23)) & np.uint32(0xFF))
+    sc = np.ldexp(np.float32(1.0), 141 - e).astype(np.float32)
+    return (v32 * sc).astype(np.float16).astype(np.float64) / np.float64(sc)
+
+
+def np_layer(host, res, hp_fp16=True, x64=None, hp_slot=False):
     """float64 restatement of the MoE layer from the oracle's routing (which
     the route tests pin) and the raw weights: each pair's SwiGLU FFN with the
-    intermediate rounded to fp16, combined in float64."""
+    intermediate rounded to fp16 (with hp_slot: through one slot scale for
+    the routed pairs and one for the shared expert, as src/qwen.c:858-886
+    does), combined in float64.  x64 replaces the fp16 x."""
     s = host["shape"]
     T, d, E, K, I, S = s["rows"], s["d"], s["experts"], s["topk"], s["inter"], s["shared"]
-    x = host["x"].view(np.float16).astype(np.float64)
+    x = host["x"].view(np.float16).astype(np.float64) if x64 is None else x64
     wgu = host["w_gate_up"].view(np.float16).astype(np.float64)
     wd = host["w_down"].view(np.float16).astype(np.float64)
     idx = res["idx"].reshape(T, K)
     wt = res["wt"].reshape(T, K).astype(np.float64)
     out = np.zeros((T, d))
+    hs = {}
     for e in range(E):
         rr, jj = np.nonzero(idx == e)
         if rr.size == 0:
             continue
         g = x[rr] @ wgu[e].T
-        h = g[:, :I] / (1 + np.exp(-g[:, :I])) * g[:, I:]
-        if hp_fp16:
+        hs[e] = (rr, jj, g[:, :I] / (1 + np.exp(-g[:, :I])) * g[:, I:])
+    if hp_slot and hs:
+        flat = slot_round(np.concatenate([h.astype(np.float32).ravel() for _, _, h in hs.values()]))
+        o = 0
+        for e, (rr, jj, h) in hs.items():
+            hs[e] = (rr, jj, flat[o:o + h.size].reshape(h.shape))
+            o += h.size
+    for e, (rr, jj, h) in hs.items():
+        if hp_fp16 and not hp_slot:
             h = h.astype(np.float16).astype(np.float64)
         np.add.at(out, rr, wt[rr, jj][:, None] * (h @ wd[e].T))
     if S:
         g = x @ host["w_sh_gate_up"].view(np.float16).astype(np.float64).T
         h = g[:, :S] / (1 + np.exp(-g[:, :S])) * g[:, S:]
-        h = h.astype(np.float16).astype(np.float64)
+        h = slot_round(h) if hp_slot else h.astype(np.float16).astype(np.float64)
         gate = 1 / (1 + np.exp(-res["proj"][:, E].astype(np.float64)))
         out += gate[:, None] * (h @ host["w_sh_down"].view(np.float16).astype(np.float64).T)
     return out
@@ -455,6 +478,55 @@ def test_layer_padding_and_scale_modes_agree():
     assert np.abs(a["out"] - b["out"]).max() <= 2e-5
     width = (b["count"].astype(np.int64) + 127) // 128 * 128
     assert np.array_equal(b["off"], (np.cumsum(width) - width).astype(np.uint32))
+
+
+def test_layer_x32_of_fp16_values_equals_fp16_input():
+    """The fp32-activation mode on fp32 copies of fp16 values: the slot cast
+    multiplies by a power of two (exact for these values, normal or not),
+    the router divides it out before the bias and the GEMMs after the
+    product, so logits, routing and output are bitwise those of the fp16
+    input in the same (slot-scaled) mode."""
+    for cfg in SMALL:
+        host = host_inputs(cfg, seed=8)
+        a = orc.layer(host, tile=1, x_scale=1, hp_scale=1)
+        h32 = dict(host, x32=orc.h2f(host["x"]), x=None)
+        b = orc.layer(h32, tile=1, x_scale=1, hp_scale=1)
+        for k in ("proj", "idx", "wt", "count", "off", "slot", "out"):
+            assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), (cfg["name"], k)
+
+
+@pytest.mark.parametrize("mag", [1e-6, 1.0, 1e6], ids=["1e-6", "1", "1e6"])
+def test_layer_x32_extreme_magnitudes_match_float64(mag):
+    """Activations far outside fp16's range: x32 = mag * N(0, 1) in fp32
+    (values not representable in fp16).  The oracle casts x with a slot, and
+    hp with a slot, where fp16 without them would flush to zero (1e-6) or
+    overflow (1e6, where hp is ~1e12).  Against a float64 layer on the same
+    routing whose only fp16 roundings are numpy's slot casts of x and hp:
+    relative L2 1e-3 and max-abs 1e-2 of the largest output."""
+    cfg = SMALL[1]
+    host = host_inputs(cfg, seed=9)
+    T, d = cfg["rows"], cfg["d"]
+    x32 = (orc.fill_normal_f32(T * d, configs.STREAM_X, 9, 1.0).reshape(T, d) * np.float32(mag)).astype(np.float32)
+    h32 = dict(host, x32=x32, x=None)
+    res = orc.layer(h32, tile=1, x_scale=1, hp_scale=1)
+    assert np.isfinite(res["out"]).all() and np.isfinite(res["proj"]).all()
+    # logits: float64 GEMM of the slot-cast x (the cast pinned above), scale divided out
+    xs = slot_round(x32)
+    w = host["w_router"].astype(np.float64)
+    proj64 = xs @ w.T
+    bound = 2e-6 * (np.abs(xs) @ np.abs(w).T)
+    assert np.all(np.abs(res["proj"] - proj64) <= bound)
+    ref = np_layer(h32, res, x64=xs, hp_slot=True)
+    err = np.abs(res["out"] - ref).max()
+    rel = np.linalg.norm(res["out"] - ref) / np.linalg.norm(ref)
+    assert rel <= 1e-3 and err <= 1e-2 * np.abs(ref).max(), (rel, err, np.abs(ref).max())
+    assert np.abs(ref).max() > (1e10 if mag > 1 else 0) and np.abs(ref).max() < (1e-8 if mag < 1 else np.inf)
+    # a mistake in the scale handling is caught: without hp's slot the fp16
+    # intermediate overflows (1e6) or flushes (1e-6)
+    if mag != 1.0:
+        with np.errstate(all="ignore"):
+            bad = np_layer(h32, res, x64=xs, hp_slot=False)
+        assert not (np.isfinite(bad).all() and np.linalg.norm(res["out"] - bad) / np.linalg.norm(ref) <= 1e-3)
 
 
 def test_skew_config_leaves_experts_empty():

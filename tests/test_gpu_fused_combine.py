@@ -11,9 +11,11 @@ shape, a shared expert with every token on one routed expert, tokens that
 select nothing, and the arrival counters over repeated calls on a workspace
 full of garbage.
 """
+import numpy as np
 import pytest
 import torch
 
+from gpu_util import MAX_ABS, REL_L2, oracle_layer, out_metrics, u32
 from rmda_moe import api, configs, inputs
 
 pytestmark = pytest.mark.gpu
@@ -63,6 +65,47 @@ def layer(ctx, inp, packed, fused, ws=None, h=None, inj=None, inj_stride=0, inj_
               h=h, inj=inj, inj_stride=inj_stride, inj_off=inj_off, hc=hc)
     ctx.sync()
     return out
+
+
+ORACLE_SHAPES = [configs.CONFIGS[k] for k in (1, 2, 3, 4, 5)] + [TEACHER]
+
+
+@pytest.mark.parametrize("cfg", ORACLE_SHAPES, ids=[c["name"] for c in ORACLE_SHAPES])
+def test_fused_combine_vs_oracle(ctx, cfg):
+    """The folded layer against the CPU oracle on every output row, with the
+    hyper-connection streams and the fp16 output written by the same call
+    (shader/moe_combine.comp:26-40, src/qwen.c:887-906): routing bit-exact,
+    out within the layer tolerance, h within twice it.  Config 4 runs the
+    compute tile, where combine16_kernel does the combine."""
+    print("fused combine vs oracle %s" % cfg["name"], flush=True)
+    seed = 0
+    inp = inputs.make_inputs(ctx, cfg, seed=seed)
+    packed = pack(ctx, inp)
+    T, d = cfg["rows"], cfg["d"]
+    hc, inj_stride, inj_off = (4, 384, 320) if cfg is TEACHER else (4, 11, 3)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    h0 = torch.randn(T, hc, d, device="cuda", generator=g)
+    inj = torch.randn(T, inj_stride, device="cuda", generator=g) * 3
+    h = h0.clone()
+    ws = inputs.workspace_for(inp["shape"])
+    ws.fill_(255)
+    out = layer(ctx, inp, packed, True, ws=ws, h=h, inj=inj, inj_stride=inj_stride, inj_off=inj_off, hc=hc)
+    ref = oracle_layer(inp, cfg, seed, tile=16)
+    views = api.ws_views(inp["shape"], ws)
+    assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(views["off"]), ref["off"]), "expert offsets"
+    assert np.array_equal(u32(views["slot"]), ref["slot"]), "permutation"
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    max_abs, rel = out_metrics(got, ref["out"])
+    print("  out max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+    gate = 2.0 / (1.0 + np.exp(-inj.cpu().numpy().astype(np.float64)[:, inj_off:inj_off + hc] / hc))
+    want = h0.cpu().numpy().astype(np.float64) + ref["out"].astype(np.float64)[:, None, :] * gate[:, :, None]
+    err = np.abs(h.cpu().numpy().astype(np.float64) - want).max()
+    print("  hc max-abs %.3g" % err, flush=True)
+    assert err <= 2 * MAX_ABS, err
 
 
 @pytest.mark.parametrize("cfg", SHAPES, ids=[c["name"] for c in SHAPES])

@@ -117,16 +117,20 @@ def test_hot_tile_against_oracle_config4(ctx):
 
 
 def test_adaptive_policy_follows_previous_call():
-    """RMDA_TILE_ADAPTIVE (the default): the first call lets the rank kernel
-    choose, later calls launch only the tile the previous call chose and have
-    the rank kernel cut its list for it, even when the new call's routing
-    would choose the other tile.  Every call's output is bitwise the
-    streaming tile's."""
+    """RMDA_TILE_ADAPTIVE (the default): the first call on a key (packed
+    weights, rows) lets the rank kernel choose, later calls on that key launch
+    only the tile its previous call chose and have the rank kernel cut its
+    list for it, even when the new call's routing would choose the other
+    tile; calls on another key neither read nor disturb that choice.  Every
+    call's output is bitwise the streaming tile's."""
     torch.cuda.set_device(0)
     c = api.Context(0)
     try:
         ins = {k: inputs.make_inputs(c, configs.CONFIGS[k], seed=0) for k in (3, 4)}
         packs = {k: pack(c, ins[k]) for k in (3, 4)}
+        # configs 3 and 4 share their weights (config 4 adds a router bias),
+        # so either packed buffer serves either input
+        assert torch.equal(packs[3].view(torch.int16), packs[4].view(torch.int16))
         # references: the streaming tile, on a context fixed to it
         ref = {}
         c.set_tile_policy(api.Context.TILE_STREAM)
@@ -134,14 +138,21 @@ def test_adaptive_policy_follows_previous_call():
             ref[k], _, n_s, n_h = packed_layer(c, ins[k], packs[k], None)
             assert n_s > 0 and n_h == 0
         c.set_tile_policy(api.Context.TILE_ADAPTIVE)
-        # (config, tile the call must use): the first call decides on the
-        # device; each later call follows the one before it
-        seq = [(4, "hot"), (4, "hot"), (3, "hot"), (3, "stream"), (4, "stream"), (4, "hot")]
-        for k, want in seq:
-            out, _, n_s, n_h = packed_layer(c, ins[k], packs[k], None)
+
+        def call(k, key, want):
+            out, _, n_s, n_h = packed_layer(c, ins[k], packs[key], None)
             got = "hot" if n_h > 0 else "stream"
-            print("adaptive: config %d used the %s tile" % (k, got), flush=True)
+            print("adaptive: config %d on weights %d used the %s tile" % (k, key, got), flush=True)
             assert got == want and (n_s == 0) == (n_h > 0)
             assert torch.equal(out.view(torch.int16), ref[k].view(torch.int16))
+
+        # one key (packs[3]): the first call decides on the device; each
+        # later call follows the one before it
+        for k, want in [(4, "hot"), (4, "hot"), (3, "hot"), (3, "stream"), (4, "stream"), (4, "hot")]:
+            call(k, 3, want)
+        # a second key (packs[4]) keeps its own choice, interleaved with the first
+        c.set_tile_policy(api.Context.TILE_ADAPTIVE)  # forget every key
+        for k, key, want in [(4, 4, "hot"), (3, 3, "stream"), (4, 4, "hot"), (3, 3, "stream"), (4, 4, "hot")]:
+            call(k, key, want)
     finally:
         c.close()

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import MAX_ABS, REL_L2, out_metrics, u32
+from gpu_util import MAX_ABS, REL_L2, oracle_layer, out_metrics, u32
 from oracle import oracle as orc
 from rmda_moe import api, configs, inputs
 
@@ -47,12 +47,11 @@ def check_layer(ctx, cfg, seed, n_sample=None):
     print("layer %s seed %d" % (cfg["name"], seed), flush=True)
     inp = inputs.make_inputs(ctx, cfg, seed=seed)
     out, views = run_layer(ctx, inp)
-    host = inputs.to_host(inp)
     T = cfg["rows"]
     sel = None
     if n_sample is not None and n_sample < T:
         sel = np.sort(np.random.default_rng(seed).choice(T, n_sample, replace=False)).astype(np.uint32)
-    ref = orc.layer(host, tile=16, rows_sel=sel, threads=16)
+    ref = oracle_layer(inp, cfg, seed, tile=16, rows_sel=sel)
     assert np.array_equal(views["proj"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
     assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
     assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
@@ -294,3 +293,139 @@ def test_layer_rejects_misaligned_pointers():
                 inputs.workspace_for(shape))
     assert e.value.code == -1
     c.close()
+
+
+@pytest.mark.parametrize("cfg", [
+    configs.CONFIGS[3],
+    configs.CONFIGS[4],
+    configs.CONFIGS[5],
+    # 3081 pairs: 4 rank blocks, a partial last one, a token's pairs straddling two
+    dict(name="count_all_tail", rows=1027, d=256, experts=40, topk=3, inter=128, shared=0, skew=False),
+    # 65 536 pairs, the largest call that routes in the rank launch (64 rank blocks)
+    dict(name="rank_all_max", rows=8192, d=256, experts=64, topk=8, inter=128, shared=128, skew=False),
+], ids=lambda c: c["name"])
+def test_layer_route_in_rank(ctx, cfg):
+    """rmda_moe_set_route_in_rank: the top-k selected inside the rank launch
+    (one workgroup per 8 tokens, the last ones to finish ranking after the
+    ticket) gives bitwise the routing, permutation and output of the separate
+    route launch, which test_layer_all_rows checks against the oracle; two
+    calls in a row, so the ticket the router clears is reused."""
+    print("route in rank %s" % cfg["name"], flush=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=6)
+    packed = ctx.pack_weights(inp["shape"], inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+    ref, vref = run_layer(ctx, inp, packed=packed)
+    ctx.set_route_in_rank(True)
+    try:
+        for _ in range(2):
+            out, v = run_layer(ctx, inp, packed=packed)
+            for k in ("idx", "wt", "count", "off", "slot"):
+                assert torch.equal(v[k].view(torch.int32), vref[k].view(torch.int32)), k
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    finally:
+        ctx.set_route_in_rank(False)
+
+
+@pytest.mark.parametrize("cfg,mag,n_sample", [
+    (configs.CONFIGS[1], 1.0, None),
+    (configs.CONFIGS[1], 1e6, None),
+    (configs.CONFIGS[1], 1e-6, None),
+    (dict(name="shared_small", rows=300, d=512, experts=16, topk=4, inter=256, shared=256, skew=False), 1e6, None),
+    (configs.CONFIGS[3], 1e6, 256),
+    (configs.CONFIGS[4], 1e-6, 256),
+], ids=["tiny_1", "tiny_1e6", "tiny_1e-6", "shared_1e6", "prefill_1e6", "skewed_1e-6"])
+def test_layer_fp32_activations(ctx, cfg, mag, n_sample):
+    """rmda_moe_layer_args_t::x32: fp32 activations of magnitude 1e-6 .. 1e6
+    (x32 = mag * N(0, 1), values not representable in fp16), through the
+    reference's slot protocol: x cast with a slot (router and gate_up divide
+    it out), hp cast with a slot (down divides it out), fp32 expert rows.
+    Against the oracle's fp32-activation mode: logits, routing and
+    permutation bit-exact; the layer output y, read from one
+    hyper-connection stream (h += y * 2 * sigmoid(0), so h = y exactly from
+    h = 0) because y itself leaves fp16's range, within relative L2 1e-3 and
+    max-abs 1e-2 of the largest output.  The fp16 output of the same call
+    equals fp16(y) where y fits.  The compute tile runs at config 4."""
+    print("x32 %s mag %g" % (cfg["name"], mag), flush=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=12)
+    shape = inp["shape"]
+    T, d = shape["rows"], shape["d"]
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x32 = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * mag
+    packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+    ws = torch.empty(api.workspace_bytes_x32(shape), dtype=torch.uint8, device="cuda")
+    ws.fill_(255)
+    h = torch.zeros(T, 1, d, dtype=torch.float32, device="cuda")
+    inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+    out = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
+    ctx.layer(shape, None, inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed, h=h, inj=inj,
+              inj_stride=1, inj_off=0, hc=1, x32=x32)
+    ctx.sync()
+    host = inputs.to_host(inp)
+    host["x"] = None
+    host["x32"] = x32.cpu().numpy()
+    sel = None
+    if n_sample is not None:
+        sel = np.sort(np.random.default_rng(12).choice(T, n_sample, replace=False)).astype(np.uint32)
+    ref = orc.layer(host, tile=16, x_scale=1, hp_scale=1, rows_sel=sel, threads=16)
+    views = api.ws_views(shape, ws)
+    assert np.array_equal(views["proj"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(views["slot"]), ref["slot"]), "permutation"
+    y = h[:, 0, :].cpu().numpy().astype(np.float64)
+    if sel is not None:
+        y = y[sel.astype(np.int64)]
+    want = ref["out"].astype(np.float64)
+    assert np.isfinite(y).all()
+    err = np.abs(y - want).max()
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+    print("  max|y| %.3g rel-L2 %.3g max-abs %.3g" % (np.abs(want).max(), rel, err), flush=True)
+    assert rel <= 1e-3 and err <= 1e-2 * np.abs(want).max(), (rel, err)
+    # the fp16 output is the same y rounded, where it fits
+    o = out.float().cpu().numpy().astype(np.float64)
+    if sel is not None:
+        o = o[sel.astype(np.int64)]
+    y32 = h[:, 0, :].cpu().numpy()
+    if sel is not None:
+        y32 = y32[sel.astype(np.int64)]
+    fits = np.abs(y32) < 65504
+    assert np.array_equal(o[fits], y32[fits].astype(np.float16).astype(np.float64))
+
+
+def test_layer_fp32_activations_of_fp16_values(ctx):
+    """x32 holding fp32 copies of the fp16 activations: the slot scale is a
+    power of two, exact on these values, so the logits and the routing are
+    bitwise the fp16-input layer's, and the output differs only by keeping
+    hp's and the expert rows' extra precision (within the layer tolerance)."""
+    cfg = configs.CONFIGS[3]
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    shape = inp["shape"]
+    ref, vref = run_layer(ctx, inp)
+    ws = torch.empty(api.workspace_bytes_x32(shape), dtype=torch.uint8, device="cuda")
+    ws.fill_(255)
+    out = torch.full((shape["rows"], shape["d"]), float("nan"), dtype=torch.float16, device="cuda")
+    ctx.layer(shape, None, inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"], None, None, out, ws,
+              x32=inp["x"].float())
+    ctx.sync()
+    v = api.ws_views(shape, ws)
+    for k in ("proj", "idx", "wt", "count", "off", "slot"):
+        assert torch.equal(v[k].view(torch.int32), vref[k].view(torch.int32)), k
+    max_abs, rel = out_metrics(out.float().cpu().numpy(), ref.float().cpu().numpy())
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_layer_fp32_activations_rejections(ctx):
+    """x and x32 together, and a workspace sized for the fp16 mode, are
+    rejected before anything is enqueued."""
+    cfg = configs.CONFIGS[1]
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    shape = inp["shape"]
+    x32 = inp["x"].float()
+    out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
+    assert api.workspace_bytes_x32(shape) > api.workspace_bytes(shape)
+    for x, ws, code in [(inp["x"], inputs.workspace_for(shape), -1), (None, inputs.workspace_for(shape), -6)]:
+        with pytest.raises(api.MoeError) as e:
+            ctx.layer(shape, x, inp["w_router"], None, inp["w_gate_up"], inp["w_down"], None, None, out, ws, x32=x32)
+        assert e.value.code == code
+        ctx.clear_error()

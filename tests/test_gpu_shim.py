@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import MAX_ABS, REL_L2, out_metrics, u32
+from gpu_util import MAX_ABS, REL_L2, oracle_layer, out_metrics, u32
 from oracle import oracle as orc
 from rmda_moe import api, configs, inputs
 
@@ -65,6 +65,52 @@ def test_moe_rec_matches_oracle_reference_mode(ctx, cfg):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
     # three fp16 scale slots were taken: x, hp and (with a shared expert) hs
     assert q.q.n_slots == (3 if cfg["shared"] else 2)
+
+
+@pytest.mark.parametrize("cfg_id,n_sample", [(3, 512), (5, 640)])
+def test_moe_rec_matches_oracle_at_bench_sizes(ctx, cfg_id, n_sample):
+    """The recording at the sizes bench.py times it (config 3: mrows 32 640
+    over 255 tiles, the live-row and fused-SwiGLU GEMMs and the 128-row hp
+    cast; config 5: 828 tiles and the shared expert) in the reference's
+    mode: routing bit-exact on every token, the output within tolerance on a
+    sample of tokens that holds a row in every used 128-row tile (one token
+    per tile, then random ones up to n_sample)."""
+    cfg = configs.CONFIGS[cfg_id]
+    print("shim %s" % cfg["name"], flush=True)
+    seed = 3
+    inp = inputs.make_inputs(ctx, cfg, seed=seed)
+    T, d, K = cfg["rows"], cfg["d"], cfg["topk"]
+    q = make_shim(ctx, inp)
+    q.scratch.fill_(255)
+    out = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
+    q.moe_rec(inp["x"].float(), T, out=out)
+    ctx.sync()
+    v = q.views(T)
+    slot = u32(v["slot"])
+    tiles = u32(v["tiles"])
+    used = np.flatnonzero(tiles != 0xFFFFFFFF)
+    tile_of_pair = np.where(slot == 0xFFFFFFFF, -1, slot.astype(np.int64) // 128)
+    first_pair = np.full(tiles.size, -1, np.int64)
+    for p in range(slot.size - 1, -1, -1):
+        if tile_of_pair[p] >= 0:
+            first_pair[tile_of_pair[p]] = p
+    assert np.all(first_pair[used] >= 0), "a used tile holds no routed row"
+    must = np.unique(first_pair[used] // K)
+    rest = np.setdiff1d(np.arange(T), must)
+    extra = np.random.default_rng(cfg_id).choice(rest, max(0, n_sample - must.size), replace=False)
+    sel = np.sort(np.concatenate([must, extra])).astype(np.uint32)
+    ref = oracle_layer(inp, cfg, seed, tile=128, hp_scale=1, x_scale=1, rows_sel=sel)
+    assert np.array_equal(v["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(v["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(v["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(v["off"]), ref["off"]), "128-row segment offsets"
+    assert np.array_equal(slot, ref["slot"]), "permutation"
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    max_abs, rel = out_metrics(got[sel.astype(np.int64)], ref["out"])
+    print("  %d used tiles, %d tokens checked; max-abs %.3g rel-L2 %.3g" % (used.size, sel.size, max_abs, rel),
+          flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
 @pytest.mark.parametrize("cfg,hc,stride,rank", [
@@ -146,6 +192,79 @@ def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
     ref16 = hp16_ref.cpu().numpy().view(np.uint16)[live]
     bad = np.flatnonzero((hp16 != ref16).any(axis=1))
     assert bad.size == 0, "hp16 rows differ: %s" % bad[:8]
+
+
+def run_documented_stages(ctx, inp, buf, xp_garbage=None):
+    """One chunk through the stage entry points in the order INTEGRATION.md
+    documents for a qwen.c that keeps its own recording (src/qwen.c:838-907):
+    slot words zeroed (:500-503), x cast with a slot for the GEMMs and
+    unscaled for the fp32 router, route, scan, xp zero-filled (:798), scatter,
+    gate_up, qwen_elem op 0, hp absmax + cast with a slot, down, combine.
+    `buf` holds every buffer and is reused across calls, as the reference's
+    scratch is."""
+    s = inp["shape"]
+    T, d, E, K, I = s["rows"], s["d"], s["experts"], s["topk"], s["inter"]
+    mrows = (T * K + E * 127 + 127) // 128 * 128
+    x = inp["x"].float()
+    amax = buf["amax"]
+    amax.zero_()
+    ctx.absmax(T * d, 0, x, amax)
+    ctx.cast_f16(T * d, 0, x, buf["a16"], amax)
+    ctx.cast_f16(T * d, 0xFFFFFFFF, x, buf["x16"], amax)
+    ctx.router(T, d, E, E, 0, buf["x16"], inp["w_router"], None, buf["p"])
+    ctx.route(T, E, K, E, buf["p"], buf["idx"], buf["wt"], buf["count"])
+    ctx.scan(E, 128, buf["count"], buf["off"], buf["tiles"], mrows // 128)
+    if xp_garbage is not None:
+        buf["xp"].view(torch.int16).fill_(xp_garbage)
+    buf["xp"].zero_()  # the reference's fill of xp before the scatter
+    ctx.scatter(T, K, d // 8, buf["idx"], buf["off"], buf["fill"], buf["a16"], buf["xp"], buf["slot"])
+    ctx.mm(mrows, 2 * I, d, 0, 0xFFFFFFFF, buf["xp"], inp["w_gate_up"], buf["g"], amax, buf["tiles"])
+    ctx.qwen_elem(mrows, I, 2 * I, 0, I, 0, 1.0, buf["g"], buf["hp"])
+    ctx.absmax(mrows * I, 1, buf["hp"], amax)
+    ctx.cast_f16(mrows * I, 1, buf["hp"], buf["hp16"], amax)
+    ctx.mm(mrows, d, I, 1, 0xFFFFFFFF, buf["hp16"], inp["w_down"], buf["ye"], amax, buf["tiles"])
+    ctx.combine_plain((T, d, K, E, E, 0, 0, 0), buf["wt"], buf["slot"], buf["ye"], buf["p"], None, buf["out"])
+    ctx.sync()
+
+
+def test_documented_stage_sequence_on_stale_scratch(ctx):
+    """The stage-by-stage sequence a qwen.c keeps when it drives the drop-ins
+    itself, on a scratch the way the reference reuses it: a first chunk
+    leaves its g, hp and ye behind (rows of tiles the second chunk does not
+    use stay stale and reach qwen_elem and the absmax, as in the reference),
+    and xp holds large finite garbage (fp16 61 280) until the documented zero
+    fill.  rmda_moe_mm computes every row of each named tile, so only that
+    fill keeps the padding rows' garbage out of g and the hp scale slot.  The
+    second chunk against the oracle in the reference's mode: routing
+    bit-exact, output within tolerance."""
+    cfg = dict(name="stages", rows=300, d=512, experts=16, topk=4, inter=256, shared=0, skew=False)
+    T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
+    mrows = (T * K + E * 127 + 127) // 128 * 128
+    f32e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float32, device="cuda")
+    u32e = lambda n: torch.full((n,), -1, dtype=torch.int32, device="cuda")
+    f16e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float16, device="cuda")
+    # buffers the stages overwrite start as NaN / all-ones; g, hp, hp16 and ye
+    # start at zero, so their only stale rows are the first chunk's
+    z32 = lambda *shp: torch.zeros(shp, dtype=torch.float32, device="cuda")
+    buf = dict(amax=u32e(16), a16=f16e(T, d), x16=f16e(T, d), p=f32e(T, E), idx=u32e(T * K), wt=f32e(T * K),
+               count=u32e(E), off=u32e(E), tiles=u32e(mrows // 128), xp=f16e(mrows, d), fill=u32e(E),
+               slot=u32e(T * K), g=z32(mrows, 2 * I), hp=z32(mrows, I),
+               hp16=torch.zeros(mrows, I, dtype=torch.float16, device="cuda"), ye=z32(mrows, d), out=f16e(T, d))
+    prev = inputs.make_inputs(ctx, cfg, seed=8)
+    run_documented_stages(ctx, prev, buf)
+    inp = inputs.make_inputs(ctx, cfg, seed=9)
+    run_documented_stages(ctx, inp, buf, xp_garbage=0x7B7B)
+    ref = orc.layer(inputs.to_host(inp), tile=128, hp_scale=1, x_scale=1)
+    assert np.array_equal(buf["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(buf["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(buf["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(buf["off"]), ref["off"]), "128-row segment offsets"
+    assert np.array_equal(u32(buf["slot"]), ref["slot"]), "permutation"
+    got = buf["out"].float().cpu().numpy()
+    assert np.isfinite(got).all()
+    max_abs, rel = out_metrics(got, ref["out"])
+    print("  max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
 def test_moe_rec_runs_twice_bitwise_and_chunks(ctx):

@@ -321,6 +321,41 @@ def test_moe_mm_vs_oracle(ctx, m, n, k, E, scaled):
     assert err <= 1e-5 * max(1.0, np.abs(ref[live]).max()), err
 
 
+@pytest.mark.parametrize("n,k", [(1536, 2048), (2048, 768)], ids=["gate_up", "down"])
+def test_moe_mm_vs_oracle_bench_size(ctx, n, k):
+    """rmda_moe_mm at the size bench.py times it: config 3's tile map (128
+    experts over mrows = 32 640, i.e. 255 tiles of 128 rows, from a scan of
+    16 384 pairs) and its K.  The GPU runs every tile; the oracle computes
+    every fifth used tile (the rest marked unused in its copy of the map),
+    whose rows are compared; unused tiles stay untouched."""
+    E, T, K = 128, 2048, 8
+    r = rng(n + k)
+    count = np.bincount(r.integers(0, E, T * K), minlength=E).astype(np.uint32)
+    mrows = (T * K + E * 127 + 127) // 128 * 128
+    ntile = mrows // 128
+    assert ntile == 255
+    _, tiles = orc.scan(count, 128, ntile)
+    used = np.flatnonzero(tiles != NONE)
+    check = used[::5]
+    tiles_ref = np.full(ntile, NONE, np.uint32)
+    tiles_ref[check] = tiles[check]
+    a = orc.fill_normal_f16(mrows * k, 11, 5, 1.0).reshape(mrows, k)
+    b = orc.fill_normal_f16(E * n * k, 12, 6, 0.02).reshape(E, n, k)
+    amax = np.zeros(4, np.uint32)
+    amax[0] = np.float32(4.1).view(np.uint32)
+    ref = orc.moe_mm(a, b, tiles_ref, n, k, sa=0, amax=amax, threads=16)
+    c = torch.full((mrows, n), 1e30, dtype=torch.float32, device="cuda")
+    ctx.mm(mrows, n, k, 0, 0xFFFFFFFF, dev(a), dev(b), c, dev(amax), dev(tiles))
+    ctx.sync()
+    got = c.cpu().numpy()
+    skip = np.repeat(tiles == NONE, 128)
+    assert np.all(got[skip] == 1e30), "rows of unused tiles must stay untouched"
+    rows = np.repeat(tiles_ref != NONE, 128)
+    err = np.abs(got[rows] - ref[rows]).max()
+    print("  %d used tiles, %d compared; max-abs %.3g" % (used.size, check.size, err), flush=True)
+    assert err <= 1e-5 * max(1.0, np.abs(ref[rows]).max()), err
+
+
 # ---------------------------------------------------------------- combine (A9) and helpers
 
 @pytest.mark.parametrize("d", [256, 2048, 258])  # 258: d % 4 != 0 takes the per-element kernel
