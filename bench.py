@@ -24,9 +24,21 @@ Prints ONE JSON line.  Besides the driver's fields it carries
                 the dense fp16 MFMA peak;
   fine_shared   (config-3 runs) BASELINE configuration 5 (512 experts,
                 top-10, shared expert);
+  mixed_load    (config-3 runs) config 3's shape with four hot experts
+                holding ~35% of the rows: the per-call tile choice against
+                each tile forced for the whole call;
+  teacher       (config-3 runs) the reference teacher's own MoE shape (d 2560,
+                512 experts, top-10, width 640 + shared) at 2048 tokens: the
+                fused layer and the reference-structured recording;
+  fp32_activations  (config-3 runs) config 3 through the slot-scaled
+                fp32-activation input;
+  alternating_layers  (config-3 runs) configs 3 and 4 alternating on one
+                context under the adaptive and the auto tile policy;
   dropin        (config-3 runs) the reference-equivalent stage entry points
-                (route, scan, scatter into xp, combine) on the same inputs,
-                with their HBM GB/s.
+                (route, scan, scatter into xp, combine, the grouped GEMM, the
+                whole recording) on the same inputs: warm legs (inputs
+                cache-resident) and cold legs (buffer sets rotated past the
+                256 MB Infinity Cache) for the copy-shaped ones.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 """
@@ -323,24 +335,37 @@ def measure_sustained(step, ctx, torch, secs, prof_calls=200):
     return res
 
 
-def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
-    """Another BASELINE configuration on the same context, timed as the main
-    line: the layer's rate, and each grouped GEMM's time, TFLOP/s and HBM
-    GB/s against the published peaks (algorithmic work; experts touched
-    counted from the run's routing).  Config 2 is the weight-streaming
-    regime (HBM-bound), config 4 the compute-bound one (hot experts)."""
+def measure_config(ctx, torch, cfg_id, steps=100, warmup=50, policy=None, x32=False):
+    """Another configuration on the same context, timed as the main line:
+    the layer's rate, and each grouped GEMM's time, TFLOP/s and HBM GB/s
+    against the published peaks (algorithmic work; experts touched counted
+    from the run's routing).  cfg_id is a BASELINE configuration number or a
+    configuration dict.  Config 2 is the weight-streaming regime
+    (HBM-bound), config 4 the compute-bound one (hot experts).  policy: a
+    tile policy for this measurement (the context's is restored after);
+    x32: the fp32-activation input (slot-scaled)."""
     from rmda_moe import api, configs, inputs
 
-    cfg = configs.CONFIGS[cfg_id]
+    cfg = configs.CONFIGS[cfg_id] if isinstance(cfg_id, int) else cfg_id
     inp = inputs.make_inputs(ctx, cfg, seed=0)
     shape = inp["shape"]
-    ws = inputs.workspace_for(shape)
+    if x32:
+        ws = torch.empty(api.workspace_bytes_x32(shape), dtype=torch.uint8, device="cuda")
+        xf = inp["x"].float()
+    else:
+        ws = inputs.workspace_for(shape)
     out = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
     packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
                               inp["w_sh_down"])
+    if policy is not None:
+        ctx.set_tile_policy(policy)
 
     def step():
-        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed)
+        if x32:
+            ctx.layer(shape, None, inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed,
+                      x32=xf)
+        else:
+            ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed)
 
     for _ in range(warmup):
         step()
@@ -363,11 +388,12 @@ def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
     counts = views["count"].cpu().numpy()
     hot = int(views["n_items_hot"].cpu().numpy()[0]) > 0
     work = configs.algorithmic_work(cfg, touched=int((counts > 0).sum()))
-    res = {"workload": "%s: T=%d d=%d experts=%d top-%d inter=%d shared=%d%s (BASELINE config %d)"
-                       % (cfg["name"], shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"],
-                          shape["shared"], " skewed" if cfg.get("skew") else "", cfg_id),
+    res = {"workload": workload_name(cfg, shape, cfg_id if isinstance(cfg_id, int) else None) +
+                       (", fp32 activations (slot-scaled)" if x32 else ""),
            "tokens/s": round(shape["rows"] / (ms * 1e-3), 1), "ms_per_step": round(ms, 5), "steps": steps,
            "experts_touched": int((counts > 0).sum()), "gemm_tile": "compute (hot experts)" if hot else "streaming"}
+    hot_min = 256
+    res["rows_on_hot_experts"] = round(float(counts[counts >= hot_min].sum()) / max(1, counts.sum()), 4)
     gemm_us = 0.0
     for k in ("gate_up", "down"):
         us = 1000.0 * stage_ms[k] / max(n_prof, 1) - event_us
@@ -377,8 +403,106 @@ def measure_config(ctx, torch, cfg_id, steps=100, warmup=50):
         res[k] = {"us": round(us, 2), "TFLOP/s": round(tf, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16_TFLOPS, 4),
                   "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     tf = work["gemm_flops"] / (gemm_us * 1e-6) / 1e12
-    res["gemm"] = {"TFLOP/s": round(tf, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+    res["gemm"] = {"us": round(gemm_us, 2), "TFLOP/s": round(tf, 1), "frac_of_fp16_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+    if policy is not None:
+        ctx.set_tile_policy(api.Context.TILE_ADAPTIVE)
     del inp, ws, out, packed
+    torch.cuda.empty_cache()
+    return res
+
+
+def workload_name(cfg, shape, cfg_id=None):
+    skew = {True: " skewed", "mixed": " mixed load"}.get(cfg.get("skew"), "")
+    return "%s: T=%d d=%d experts=%d top-%d inter=%d shared=%d%s%s" % (
+        cfg["name"], shape["rows"], shape["d"], shape["experts"], shape["topk"], shape["inter"], shape["shared"],
+        skew, " (BASELINE config %d)" % cfg_id if cfg_id else "")
+
+
+def measure_mixed(ctx, torch):
+    """Config 3's shape with four hot experts holding ~35% of the rows (the
+    rest on 124 cold experts): the per-call tile choice (the streaming tile,
+    since the hot bucket holds under half the rows) against each tile forced
+    for the whole call.  The gap is what a per-expert tile choice inside one
+    call could win at most."""
+    from rmda_moe import api, configs
+    res = {"per_call_choice": measure_config(ctx, torch, configs.MIXED, policy=api.Context.TILE_ADAPTIVE),
+           "stream_tile": measure_config(ctx, torch, configs.MIXED, policy=api.Context.TILE_STREAM),
+           "compute_tile": measure_config(ctx, torch, configs.MIXED, policy=api.Context.TILE_HOT)}
+    best = min(res["stream_tile"]["gemm"]["us"], res["compute_tile"]["gemm"]["us"])
+    res["gemm_us_per_call_choice_over_best_forced"] = round(res["per_call_choice"]["gemm"]["us"] / best, 4)
+    return res
+
+
+def measure_alternating(ctx, torch, pairs=100, warmup=20):
+    """Two layers on one context, config 3 (streaming tile) and config 4
+    (compute tile) alternating call by call, as a model's layers would:
+    ms per layer call under RMDA_TILE_ADAPTIVE (each layer's own last choice,
+    keyed by its packed weights) and RMDA_TILE_AUTO (both tiles launched)."""
+    from rmda_moe import api, configs, inputs
+    L = []
+    for k in (3, 4):
+        inp = inputs.make_inputs(ctx, configs.CONFIGS[k], seed=0)
+        sh = inp["shape"]
+        packed = ctx.pack_weights(sh, inp["w_router"], inp["w_gate_up"], inp["w_down"])
+        L.append((inp, sh, packed, inputs.workspace_for(sh),
+                  torch.empty(sh["rows"], sh["d"], dtype=torch.float16, device="cuda")))
+    res = {"what": "config 3 and config 4 layers alternating on one context, ms per layer call"}
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for name, pol in (("adaptive", api.Context.TILE_ADAPTIVE), ("auto", api.Context.TILE_AUTO)):
+        ctx.set_tile_policy(pol)
+
+        def pair():
+            for inp, sh, packed, ws, out in L:
+                ctx.layer(sh, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, out, ws,
+                          packed=packed)
+        for _ in range(warmup):
+            pair()
+        ctx.sync()
+        e0.record()
+        for _ in range(pairs):
+            pair()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_ms_per_layer"] = round(e0.elapsed_time(e1) / (2 * pairs), 5)
+    ctx.set_tile_policy(api.Context.TILE_ADAPTIVE)
+    del L
+    torch.cuda.empty_cache()
+    return res
+
+
+def measure_teacher(ctx, torch, steps=50, warmup=20):
+    """The reference teacher's own MoE shape (d 2560, 512 experts, top-10,
+    width 640 with a shared expert; src/qwen.c:11-37) at the training batch
+    of 2048 tokens: the fused layer on packed weights, and the reference's
+    recording (rmda_qwen_moe_rec: 128-row segments, slot-scaled casts, fp32
+    rows, hyper-connection streams out) on the HF-layout weights."""
+    from rmda_moe import api, configs, inputs
+    cfg = configs.TEACHER
+    res = {"fused": measure_config(ctx, torch, cfg, steps=steps, warmup=warmup)}
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    s = inp["shape"]
+    T, d = s["rows"], s["d"]
+    hc, hc_pad, hc_rank = 4, 384, 320  # MDA_QWEN_HC, MDA_QWEN_HC_PAD, cfg.hc_rank (src/qwen.h:20-21)
+    qm = api.QwenMoe(ctx, s, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                     inp["w_sh_down"], hc=hc, hc_rank=hc_rank, inj_stride=hc_pad)
+    x32 = inp["x"].float()
+    h = torch.zeros(T, hc, d, dtype=torch.float32, device="cuda")
+    inj = torch.zeros(T, hc_pad, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        qm.moe_rec(x32, T, inj=inj, h=h)
+    ctx.sync()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        qm.moe_rec(x32, T, inj=inj, h=h)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    res["qwen_moe_rec"] = {"ms_per_step": round(ms, 4), "tokens/s": round(T / (ms * 1e-3), 1),
+                           "what": "rmda_qwen_moe_rec at the teacher shape, HF weights, 4 hc streams"}
+    del qm, x32, h, inj, inp
     torch.cuda.empty_cache()
     return res
 
@@ -420,7 +544,11 @@ def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
         ("combine_plain", lambda: ctx.combine_plain(fields, wt, slot, y, proj, None, out),
          T * K * d * 4 + T * K * 8 + T * d * 2),
     ]
-    res = {"workload": "BASELINE config 3 inputs, reference segments P=%d (mrows %d), fp32 expert outputs" % (P, mrows)}
+    res = {"workload": "BASELINE config 3 inputs, reference segments P=%d (mrows %d), fp32 expert outputs" % (P, mrows),
+           "rates": "algorithmic bytes / time.  The plain legs repeat one call on the same buffers, so inputs "
+                    "that fit the 256 MB Infinity Cache (scatter's x, combine's 134 MB of y) are served from it "
+                    "(cache_resident); the *_cold legs rotate through buffer sets totalling over 256 MB so every "
+                    "call reads HBM, and only they carry frac_of_hbm_peak"}
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     for name, fn, nbytes in stages:
@@ -436,7 +564,39 @@ def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
         res[name] = {"us": round(us, 2)}
         if nbytes:
             gbs = nbytes / (us * 1e-6) / 1e9
-            res[name].update({"bytes": nbytes, "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)})
+            res[name].update({"bytes": nbytes, "GB/s": round(gbs, 1),
+                              "cache_resident": "inputs re-read every call (Infinity Cache)"})
+    # cold: NSET buffer sets used in turn, so a set's bytes were evicted by
+    # the other sets' since its last use (each combine set holds 134 MB of y,
+    # each scatter set 134 MB of xp and its own 8 MB of x)
+    NSET = 3
+    ys = [torch.randn(mrows, d, dtype=torch.float32, device=dev) for _ in range(NSET)]
+    hs = [torch.zeros(T, HC, d, dtype=torch.float32, device=dev) for _ in range(NSET)]
+    xps = [torch.zeros(mrows, d, dtype=torch.float16, device=dev) for _ in range(NSET)]
+    xs = [inp["x"].clone() for _ in range(NSET)]
+    cold = [
+        ("scatter_cold", lambda i: ctx.scatter(T, K, d // 8, idx, off, fill, xs[i], xps[i], slot), res["scatter"]["bytes"]),
+        ("combine_hc_cold", lambda i: ctx.combine(fields, wt, slot, ys[i], proj, None, inj, hs[i]),
+         res["combine_hc"]["bytes"]),
+        ("combine_plain_cold", lambda i: ctx.combine_plain(fields, wt, slot, ys[i], proj, None, out),
+         res["combine_plain"]["bytes"]),
+    ]
+    for name, fn, nbytes in cold:
+        for i in range(2 * NSET):
+            fn(i % NSET)
+        ctx.sync()
+        e0.record()
+        for i in range(iters):
+            fn(i % NSET)
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / iters
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     "what": "%d buffer sets in turn (%.0f MB), every call's inputs from HBM"
+                             % (NSET, NSET * (ys[0].numel() * 4 if "combine" in name else xps[0].numel() * 2) / 1e6)}
+    del ys, hs, xps, xs
     # the reference's grouped GEMM (matmul_f16_moe): 128-row tiles of xp,
     # HF [E][n][k] weights, fp32 C; gate_up then down on a fp16 stand-in for hp16
     I = s["inter"]
@@ -482,9 +642,9 @@ def measure_dropins(ctx, torch, inp, iters=50, warmup=10):
     res["qwen_moe_rec"] = {"ms_per_step": round(ms, 4), "tokens/s": round(T / (ms * 1e-3), 1),
                            "what": "rmda_qwen_moe_rec: the reference's recording stage by stage, HF weights"}
     del qm, x32
-    sc_b = res["scatter"]["bytes"] + res["combine_hc"]["bytes"]
-    sc_us = res["scatter"]["us"] + res["combine_hc"]["us"]
-    res["scatter+combine_hc_GB/s"] = round(sc_b / (sc_us * 1e-6) / 1e9, 1)
+    sc_b = res["scatter_cold"]["bytes"] + res["combine_hc_cold"]["bytes"]
+    sc_us = res["scatter_cold"]["us"] + res["combine_hc_cold"]["us"]
+    res["scatter+combine_hc_cold_GB/s"] = round(sc_b / (sc_us * 1e-6) / 1e9, 1)
     del proj, idx, wt, count, off, tiles, fill, slot, xp, y, h, inj, out
     torch.cuda.empty_cache()
     return res
@@ -673,7 +833,10 @@ def main():
     gemm = {"TFLOP/s": round(gemm_tf, 1), "frac_of_fp16_peak": round(gemm_tf / PEAK_FP16_TFLOPS, 4),
             "ai_flop_per_byte": round(ai, 1), "ceiling_TFLOP/s": round(ceiling, 1),
             "frac_of_ceiling": round(gemm_tf / ceiling, 4), "experts_touched": touched}
-    hbm_small = {"combine_GB/s": stages.get("combine", {}).get("GB/s")}
+    # the layer's combine reads the 67 MB of fp16 rows the down GEMM wrote
+    # just before, from the Infinity Cache: a cache-resident rate
+    hbm_small = {"combine_GB/s": stages.get("combine", {}).get("GB/s"),
+                 "combine_inputs": "cache_resident: the fp16 expert rows written by the down GEMM just before"}
     stages["event_interval_us"] = round(event_us, 2)
 
     if args.calib_copy:
@@ -693,6 +856,10 @@ def main():
     if args.config == 3 and not args.no_others:
         others["skew"] = measure_config(ctx, torch, 4)
         others["fine_shared"] = measure_config(ctx, torch, 5)
+        others["mixed_load"] = measure_mixed(ctx, torch)
+        others["teacher"] = measure_teacher(ctx, torch)
+        others["fp32_activations"] = measure_config(ctx, torch, 3, x32=True)
+        others["alternating_layers"] = measure_alternating(ctx, torch)
     dropin = measure_dropins(ctx, torch, inp) if (args.config == 3 and not args.no_dropin) else None
 
     cpu = None
@@ -720,9 +887,7 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (counter-hash N(0,1) activations, N(0,0.02) weights, seed 0)",
-        "config": {"workload": "%s: T=%d d=%d experts=%d top-%d inter=%d shared=%d%s (BASELINE config %d)"
-                               % (cfg["name"], T, shape["d"], shape["experts"], shape["topk"], shape["inter"],
-                                  shape["shared"], " skewed" if cfg.get("skew") else "", args.config),
+        "config": {"workload": workload_name(cfg, shape, args.config),
                    "tokens": T, "d": shape["d"], "experts": shape["experts"], "topk": shape["topk"],
                    "inter": shape["inter"], "shared": shape["shared"], "parallelism": "single GPU"},
         "wall_ms_per_step": round(1000.0 * wall / args.steps, 5),
@@ -734,11 +899,15 @@ def main():
         "weights": "HF layout" if args.hf_layout else "packed once before timing (%.1f ms, host-timed)" % pack_ms,
         "roofline": roof,
         "gemm": gemm,
-        "hbm": hbm_small,
+        "bandwidth": hbm_small,
         "stages": stages,
         "decode": decode,
         "skew": others.get("skew"),
         "fine_shared": others.get("fine_shared"),
+        "mixed_load": others.get("mixed_load"),
+        "teacher": others.get("teacher"),
+        "fp32_activations": others.get("fp32_activations"),
+        "alternating_layers": others.get("alternating_layers"),
         "dropin": dropin,
         "cpu_baseline": cpu,
     }
@@ -758,7 +927,8 @@ def main():
         if hbm_small.get("combine_GB/s"):
             hbm_small["combine_frac_of_measured_copy"] = round(hbm_small["combine_GB/s"] / cp, 4)
         if dropin is not None:
-            for k in ("scatter", "combine_hc", "combine_plain"):
+            for k in ("scatter", "combine_hc", "combine_plain", "scatter_cold", "combine_hc_cold",
+                      "combine_plain_cold"):
                 if "GB/s" in dropin.get(k, {}):
                     dropin[k]["frac_of_measured_copy"] = round(dropin[k]["GB/s"] / cp, 4)
     ctx.close()

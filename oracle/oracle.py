@@ -11,7 +11,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmoe_oracle.so")
+# RMDA_ORACLE_LIB: another build of the same source (the sanitized one of tests/asan)
+LIB_PATH = os.environ.get("RMDA_ORACLE_LIB") or os.path.join(HERE, "libmoe_oracle.so")
 REF_HASH_PATH = os.path.join(HERE, "_ref", "libref_hash.so")
 REF_SAFET_PATH = os.path.join(HERE, "_ref", "libref_safet.so")
 

@@ -547,10 +547,14 @@ __global__ __launch_bounds__(NT) void rank_kernel(rmda_rank_args_t a) {
     }
     uint32_t *const n_out = hot ? a.n_items_hot : a.n_items;
     if (hot) {
-        // The compute tile deals contiguous runs of tasks to each XCD, so its
-        // list is in expert order (an expert's items adjacent, the shared
-        // group last): the CUs of one XCD then work on the same expert's
-        // weight tiles at the same time and share them in their L2.
+        // The compute tile's list is in expert order (an expert's items
+        // adjacent, the shared group last), not sorted by rows: its default
+        // schedule (task_sched_t) deals whole items to the XCDs in snake
+        // order, and a compute-tile task costs about the same whatever its
+        // rows (the weight slab's fill dominates; sorting by rows measured no
+        // better).  The alternative schedule (chunk_sched_t) deals contiguous
+        // runs of this order to each XCD, so that one XCD's CUs share an
+        // expert's weight tiles in their L2.
         const uint32_t ni0 = (c0 + bm - 1u) / bm;
         const uint32_t ni1 = (c1 + bm - 1u) / bm;
         uint32_t n_routed = 0;

@@ -12,6 +12,9 @@ ROOT_DIR = os.path.dirname(PKG_DIR)              # r-mda_amd/
 REPO_DIR = os.path.dirname(ROOT_DIR)
 CSRC_DIR = os.path.join(ROOT_DIR, "csrc")
 LIB_PATH = os.path.join(CSRC_DIR, "librmda_moe.so")
+# A partial build of the library in its place (the sanitized safetensors
+# reader of tests/asan): only the entry points it exports get bound.
+PARTIAL_LIB = os.environ.get("RMDA_MOE_PARTIAL_LIB")
 HEADER_PATH = os.path.join(REPO_DIR, "include", "rmda_moe.h")
 
 _u32 = ctypes.c_uint32
@@ -186,8 +189,10 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError("librmda_moe.so is missing at %s: build it with __graft_entry__.build() "
                                "(there is no CPU fallback)" % LIB_PATH)
-        L = ctypes.CDLL(LIB_PATH)
+        L = ctypes.CDLL(PARTIAL_LIB or LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
+            if PARTIAL_LIB and not hasattr(L, name):
+                continue
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args

@@ -33,6 +33,21 @@ CONFIGS = {
 
 HEADLINE = 3
 
+# The reference teacher's own MoE shape (src/qwen.c:11-37, src/qwen.h:20-21):
+# hidden 2560, 512 experts, top-10, expert and shared width 640; rows = the
+# repo's training batch of 8 x 256 tokens
+TEACHER = dict(name="teacher", rows=2048, d=2560, experts=512, topk=10, inter=640, shared=640, skew=False)
+
+# Config 3's shape with a mixed expert load: MIXED_HOT experts get a router
+# bias of MIXED_BIAS, which puts each of them in about 70% of the tokens'
+# top-8, so together they hold about 35% of the rows (~1400 each, hot) and
+# the other 124 experts about 85 rows each (cold).  Neither tile's bucket
+# holds every row: the per-call tile choice has to leave one bucket on the
+# other bucket's tile.
+MIXED_HOT = (3, 40, 77, 114)
+MIXED_BIAS = 2.0
+MIXED = dict(name="mixed", rows=2048, d=2048, experts=128, topk=8, inter=768, shared=0, skew="mixed")
+
 _M64 = (1 << 64) - 1
 
 
@@ -56,6 +71,22 @@ def skew_bias(experts, seed=0):
         j = hash_u64(STREAM_PERM, seed, i) % (i + 1)
         rank[i], rank[j] = rank[j], rank[i]
     return np.array([3.0 * math.log(1.0 / (r ** 1.2)) for r in rank], dtype=np.float32)
+
+
+def mixed_bias(experts):
+    """Router bias of the MIXED workload: MIXED_BIAS on MIXED_HOT, 0 elsewhere."""
+    b = np.zeros(experts, dtype=np.float32)
+    b[[e for e in MIXED_HOT if e < experts]] = np.float32(MIXED_BIAS)
+    return b
+
+
+def router_bias(cfg, seed=0):
+    """The router bias a configuration's inputs carry, or None."""
+    if cfg.get("skew") == "mixed":
+        return mixed_bias(cfg["experts"])
+    if cfg.get("skew"):
+        return skew_bias(cfg["experts"], seed)
+    return None
 
 
 def shape_of(cfg):

@@ -13,8 +13,9 @@ def make_inputs(ctx, cfg, seed=0, device="cuda"):
         ctx.fill_normal(t, stream, seed, std)
         out[name] = t
     out["bias"] = None
-    if cfg.get("skew"):
-        out["bias"] = torch.from_numpy(configs.skew_bias(cfg["experts"], seed)).to(device)
+    bias = configs.router_bias(cfg, seed)
+    if bias is not None:
+        out["bias"] = torch.from_numpy(bias).to(device)
     for name in ["w_sh_gate_up", "w_sh_down"]:
         out.setdefault(name, None)
     return out

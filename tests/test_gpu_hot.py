@@ -81,6 +81,8 @@ SHAPES = [
     dict(name="skew_k1", rows=900, d=512, experts=24, topk=1, inter=256, shared=256, skew=True),
     dict(name="ragged", rows=203, d=512, experts=8, topk=2, inter=1024, shared=0, skew=False),
     dict(name="e130_k7", rows=129, d=768, experts=130, topk=7, inter=384, shared=0, skew=False),
+    # four hot experts hold ~35% of the rows, 124 cold ones the rest
+    configs.MIXED,
 ]
 
 
@@ -98,6 +100,31 @@ def test_hot_tile_bitwise(ctx, cfg):
     assert n_stream1 == 0 and n_hot > 0
     assert torch.isfinite(out_h.float()).all()
     assert torch.equal(out_h.view(torch.int16), out_s.view(torch.int16)), "compute tile differs from streaming tile"
+
+
+def test_mixed_load_bucket_and_oracle(ctx):
+    """The mixed load: the hot bucket (four experts, ~35% of the rows) holds
+    under half the rows, so the call runs the streaming tile; forced onto the
+    compute tile it gives the same bits; and the output is within tolerance
+    of the oracle on a sample of tokens."""
+    cfg = configs.MIXED
+    inp = inputs.make_inputs(ctx, cfg, seed=0)
+    packed = pack(ctx, inp)
+    out, views, n_stream, n_hot = packed_layer(ctx, inp, packed, 256)
+    counts = u32(views["count"]).astype(np.int64)
+    frac = counts[counts >= 256].sum() / counts.sum()
+    print("mixed: hot experts %d, rows on them %.3f" % ((counts >= 256).sum(), frac), flush=True)
+    assert (counts >= 256).sum() == len(configs.MIXED_HOT) and 0.25 < frac < 0.5
+    assert n_hot == 0 and n_stream > 0
+    out_h, _, n_stream1, n_hot1 = packed_layer(ctx, inp, packed, 1)
+    assert n_stream1 == 0 and n_hot1 > 0
+    assert torch.equal(out_h.view(torch.int16), out.view(torch.int16))
+    ctx.set_hot_rows(256)
+    sel = np.sort(np.random.default_rng(1).choice(cfg["rows"], 256, replace=False)).astype(np.uint32)
+    ref = orc.layer(inputs.to_host(inp), tile=16, rows_sel=sel, threads=16)
+    assert np.array_equal(u32(views["idx"]), ref["idx"])
+    max_abs, rel = out_metrics(out.float().cpu().numpy()[sel.astype(np.int64)], ref["out"])
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
 def test_hot_tile_against_oracle_config4(ctx):

@@ -87,3 +87,53 @@ def test_static_layer_rejections():
         run_pair(ctx, cfg, seed=2)
     finally:
         ctx.close()
+
+
+def test_static_layer_allocates_nothing_and_captures_in_a_graph():
+    """The header's two promises.  (1) The call allocates nothing: the
+    device's free bytes are unchanged across repeated static calls.  (2) It
+    enqueues only kernels, so it can be captured in a HIP graph: the graph is
+    replayed several times, with eager work and synchronisation between the
+    replays, and every replay's output equals rmda_moe_layer's bitwise."""
+    torch.cuda.set_device(0)
+    ctx = api.Context(0)
+    try:
+        cfg = configs.CONFIGS[2]
+        inp = inputs.make_inputs(ctx, cfg, seed=3)
+        shape = inp["shape"]
+        packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                                  inp["w_sh_down"])
+        ws = inputs.workspace_for(shape)
+        ref = torch.empty(shape["rows"], shape["d"], dtype=torch.float16, device="cuda")
+        ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, ref, ws, packed=packed)
+        got = torch.full_like(ref, float("nan"))
+        ctx.layer_static(shape, inp["x"], inp["w_router"], inp["bias"], got, packed=packed)
+        ctx.sync()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+        free0, _ = torch.cuda.mem_get_info()
+        for _ in range(5):
+            ctx.layer_static(shape, inp["x"], inp["w_router"], inp["bias"], got, packed=packed)
+        ctx.sync()
+        free1, _ = torch.cuda.mem_get_info()
+        assert free1 == free0, "static layer changed the device's free memory: %d -> %d" % (free0, free1)
+        # capture on a side stream; the context issues on it during the capture
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        out_g = torch.full_like(ref, float("nan"))
+        ctx.set_stream(s)
+        try:
+            with torch.cuda.graph(graph, stream=s):
+                ctx.layer_static(shape, inp["x"], inp["w_router"], inp["bias"], out_g, packed=packed)
+        finally:
+            ctx.set_stream(torch.cuda.current_stream())
+        for rep in range(4):
+            out_g.fill_(float("nan"))  # eager work between replays
+            ctx.layer(shape, inp["x"], inp["w_router"], inp["bias"], None, None, None, None, got, ws, packed=packed)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_g.view(torch.int16), ref.view(torch.int16)), "graph replay %d" % rep
+        del graph
+    finally:
+        ctx.close()
