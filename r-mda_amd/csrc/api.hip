@@ -234,7 +234,7 @@ void prof_skip(rmda_moe_ctx_t *c, uint32_t st) {
 
 struct LayerPlan {
     size_t proj, idx, wt, lrank, slot, rowtok, count, off, hist, done, n_items, n_items_hot, items, hp, fc_cnt, xs16,
-        xpart, xslot, hslot, ye, total;
+        xpart, xslot, hslot, hparts, ye, total;
     uint32_t ps, npairs, nblocks, max_items, sh_rows, sh_row0, groups_rows;
 };
 
@@ -314,6 +314,7 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s, bool x32 = false) {
     p.xpart = take(x32 ? (size_t)RMDA_XCAST_PARTS * 4 : 0);
     p.xslot = take(x32 ? 4 : 0);
     p.hslot = take(x32 ? 4 : 0);
+    p.hparts = take(x32 ? RMDA_AMAX_BYTES : 0);  // gate_up's partial SwiGLU absmax words
     p.ye = take(x32 ? (size_t)p.groups_rows * std::max(s->d, s->inter) * 4 : (size_t)p.groups_rows * s->d * 2);
     p.total = o;
     return p;
@@ -1064,14 +1065,15 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     rc = prof_mark(ctx, 0);
     // fp32 activations: x's absmax into a fresh slot and the scaled fp16 cast
     // the router and gate_up read (absmax.comp + cast_f16.comp,
-    // src/qwen.c:517-539, :844); the second launch also clears hp's slot
+    // src/qwen.c:517-539, :844); the second launch also clears gate_up's
+    // partial absmax words
     if (rc == RMDA_OK && x32) {
         rc = hip_check(ctx, rmda_launch_x_absmax(s, args->x32, (size_t)T * d, at<uint32_t>(ws, p.xpart)),
                        "layer x absmax");
         if (rc == RMDA_OK) {
             rc = hip_check(ctx,
                            rmda_launch_x_cast(s, args->x32, (size_t)T * d, at<uint32_t>(ws, p.xpart),
-                                              at<uint16_t>(ws, p.xs16), xslot, hslot),
+                                              at<uint16_t>(ws, p.xs16), xslot, at<uint32_t>(ws, p.hparts)),
                            "layer x cast");
         }
     }
@@ -1204,7 +1206,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.a = xin;
         g.xscale = xslot;
         g.hp32 = x32 ? at<float>(ws, p.ye) : nullptr;  // fp32 SwiGLU output, cast below
-        g.hp_amax = hslot;
+        g.hp_amax = x32 ? at<uint32_t>(ws, p.hparts) : nullptr;
         g.rowtok = rowtok;
         g.a_rows = T;
         g.lda = d;
@@ -1232,8 +1234,9 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     // x32: hp's slot-scaled fp16 cast (src/qwen.c:858-877), routed and shared rows
     if (rc == RMDA_OK && x32) {
         rc = hip_check(ctx,
-                       rmda_launch_hp_cast(s, at<float>(ws, p.ye), hp, hslot, at<uint32_t>(ws, p.off),
-                                           at<uint32_t>(ws, p.count), E, I, p.sh_row0, p.sh_rows),
+                       rmda_launch_hp_cast(s, at<float>(ws, p.ye), hp, at<uint32_t>(ws, p.hparts), hslot,
+                                           at<uint32_t>(ws, p.off), at<uint32_t>(ws, p.count), E, I, p.sh_row0,
+                                           p.sh_rows),
                        "layer hp cast");
     }
     if (rc == RMDA_OK) {

@@ -148,13 +148,24 @@ __device__ __forceinline__ float rmda_slot_inv(const uint32_t *amax) {
     return ldexpf(1.0f, (int)((u >> 23) & 0xffu) - 141);
 }
 
-// A wave's largest |v| into *amax (absmax.comp's atomicMax on the float bits
-// of non-negative values; each lane passes fmaxf over its values, so NaN is
-// skipped as absmax_kernel skips it).  The whole wave must be active.
-__device__ __forceinline__ void rmda_wave_amax(uint32_t *amax, float m) {
+// The slot-scaled mode's SwiGLU absmax is gathered in RMDA_AMAX_PARTS partial
+// words, RMDA_AMAX_STRIDE words apart (one 128-byte line each), which the hp
+// cast folds, so that the GEMM waves' device-scope atomics spread over 64
+// lines instead of queueing on one word.
+#define RMDA_AMAX_PARTS 64u
+#define RMDA_AMAX_STRIDE 32u
+#define RMDA_AMAX_BYTES (RMDA_AMAX_PARTS * RMDA_AMAX_STRIDE * 4u)
+
+// A wave's largest |v| into its partial word of parts (absmax.comp's
+// atomicMax on the float bits of non-negative values; each lane passes fmaxf
+// over its values, so NaN is skipped as absmax_kernel skips it).  Called once
+// per wave at the end of a persistent kernel, with the lane's maximum over
+// all its tasks.  The whole wave must be active.
+__device__ __forceinline__ void rmda_wave_amax(uint32_t *parts, float m) {
     const uint32_t r = rmda_wave_red_u32<true>(__builtin_bit_cast(uint32_t, m));
     if (threadIdx.x % RMDA_WAVE == 0) {
-        atomicMax(amax, r);
+        const uint32_t part = (blockIdx.x * 13u + threadIdx.x / RMDA_WAVE) % RMDA_AMAX_PARTS;
+        atomicMax(parts + part * RMDA_AMAX_STRIDE, r);
     }
 }
 
@@ -472,8 +483,8 @@ struct rmda_gemm_args_t {
     // The fused layer's slot-scaled mode (fp32 activations; all NULL
     // otherwise).  SWIGLU: g and u are multiplied by rmda_slot_inv(xscale)
     // before SiLU, and with hp32 set the SwiGLU output goes to hp32 as fp32
-    // (same blocked index as the fp16 hp) with its absmax into *hp_amax
-    // instead of fp16 to out.  F16: the output is multiplied by
+    // (same blocked index as the fp16 hp) instead of fp16 to out, and its
+    // absmax into the partial words hp_amax (RMDA_AMAX_BYTES, zeroed before).  F16: the output is multiplied by
     // rmda_slot_inv(yscale), and with ye32 set it is stored to ye32 as fp32
     // instead of fp16 to out.
     const uint32_t *xscale;
@@ -583,16 +594,17 @@ hipError_t rmda_launch_fill_normal(hipStream_t s, void *dst, size_t n, int f16, 
 // zero-filled slot word needed beforehand): part[b] = the absmax bits of
 // block b's share of x (nparts blocks), then every block folds the parts,
 // casts its share of x with the slot scale into x16, and block 0 stores the
-// absmax to *x_slot and zero to *zero_slot.  n % 4 == 0, x and x16 16-byte
-// aligned.
+// absmax to *x_slot and zeroes the RMDA_AMAX_PARTS partial words at
+// hp_parts.  n % 4 == 0, x and x16 16-byte aligned.
 #define RMDA_XCAST_PARTS 256u
 hipError_t rmda_launch_x_absmax(hipStream_t s, const float *x, size_t n, uint32_t *part);
 hipError_t rmda_launch_x_cast(hipStream_t s, const float *x, size_t n, const uint32_t *part, uint16_t *x16,
-                              uint32_t *x_slot, uint32_t *zero_slot);
-// hp16[i] = fp16(hp32[i] * scale(*slot)) over the blocked hp of the slot-scaled
+                              uint32_t *x_slot, uint32_t *hp_parts);
+// hp16[i] = fp16(hp32[i] * scale(amax)) over the blocked hp of the slot-scaled
 // mode, for the routed rows [0, off[E-1] + count[E-1] rounded up to 16) and,
 // when sh_rows > 0, the shared expert's rows [sh_row0, sh_row0 + sh_rows
-// rounded up to 16); inter % 4 == 0.
-hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *slot,
-                               const uint32_t *off, const uint32_t *count, uint32_t experts, uint32_t inter,
-                               uint32_t sh_row0, uint32_t sh_rows);
+// rounded up to 16); inter % 4 == 0.  amax is the fold of the partial words
+// at hp_parts, which block 0 also stores to *slot for the down GEMM.
+hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *hp_parts,
+                               uint32_t *slot, const uint32_t *off, const uint32_t *count, uint32_t experts,
+                               uint32_t inter, uint32_t sh_row0, uint32_t sh_rows);

@@ -514,7 +514,7 @@ __global__ __launch_bounds__(256) void x_absmax_kernel(const float4 *__restrict_
 // patterns order as the values do), then cast_f16.comp over its share
 __global__ __launch_bounds__(256) void x_cast_kernel(const float4 *__restrict__ x, size_t n4,
                                                      const uint32_t *__restrict__ part, uint2 *__restrict__ x16,
-                                                     uint32_t *__restrict__ x_slot, uint32_t *__restrict__ zero_slot) {
+                                                     uint32_t *__restrict__ x_slot, uint32_t *__restrict__ hp_parts) {
     __shared__ uint32_t s_amax;
     if (threadIdx.x < RMDA_WAVE) {
         uint32_t m = 0;
@@ -528,9 +528,13 @@ __global__ __launch_bounds__(256) void x_cast_kernel(const float4 *__restrict__ 
     }
     __syncthreads();
     const uint32_t amax = s_amax;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        *x_slot = amax;
-        *zero_slot = 0u;
+    if (blockIdx.x == 0) {
+        if (threadIdx.x == 0) {
+            *x_slot = amax;
+        }
+        if (threadIdx.x < RMDA_AMAX_PARTS) {
+            hp_parts[threadIdx.x * RMDA_AMAX_STRIDE] = 0u;
+        }
     }
     const float sc = amax_scale(amax);
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
@@ -538,17 +542,31 @@ __global__ __launch_bounds__(256) void x_cast_kernel(const float4 *__restrict__ 
     }
 }
 
-// the blocked hp: 16-row groups are contiguous runs of 16 * inter values
+// every block folds the GEMM's partial absmax words, block 0 stores the fold
+// to the slot the down GEMM reads; the blocked hp: 16-row groups are
+// contiguous runs of 16 * inter values
 __global__ __launch_bounds__(256) void hp_cast_kernel(const float4 *__restrict__ hp32, uint2 *__restrict__ hp16,
-                                                      const uint32_t *__restrict__ slot,
-                                                      const uint32_t *__restrict__ off,
+                                                      const uint32_t *__restrict__ hp_parts,
+                                                      uint32_t *__restrict__ slot, const uint32_t *__restrict__ off,
                                                       const uint32_t *__restrict__ count, uint32_t experts,
                                                       uint32_t inter, uint32_t sh_row0, uint32_t sh_rows) {
+    static_assert(RMDA_AMAX_PARTS == RMDA_WAVE, "one partial word per lane");
+    __shared__ uint32_t s_amax;
+    if (threadIdx.x < RMDA_WAVE) {
+        const uint32_t m = rmda_wave_red_u32<true>(hp_parts[threadIdx.x * RMDA_AMAX_STRIDE]);
+        if (threadIdx.x == 0) {
+            s_amax = m;
+            if (blockIdx.x == 0) {
+                *slot = m;
+            }
+        }
+    }
+    __syncthreads();
     const uint32_t routed_end = off[experts - 1] + (count[experts - 1] + 15u) / 16u * 16u;
     const size_t n_r = (size_t)routed_end * inter / 4;
     const size_t s0 = (size_t)sh_row0 * inter / 4;
     const size_t n_s = (size_t)((sh_rows + 15u) / 16u * 16u) * inter / 4;
-    const float sc = amax_scale(*slot);
+    const float sc = amax_scale(s_amax);
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_r + n_s; i += (size_t)gridDim.x * 256) {
         const size_t j = i < n_r ? i : s0 + (i - n_r);
         hp16[j] = cast4(hp32[j], sc);
@@ -564,16 +582,17 @@ hipError_t rmda_launch_x_absmax(hipStream_t s, const float *x, size_t n, uint32_
 }
 
 hipError_t rmda_launch_x_cast(hipStream_t s, const float *x, size_t n, const uint32_t *part, uint16_t *x16,
-                              uint32_t *x_slot, uint32_t *zero_slot) {
+                              uint32_t *x_slot, uint32_t *hp_parts) {
     hipLaunchKernelGGL(x_cast_kernel, dim3(RMDA_XCAST_PARTS), dim3(256), 0, s, reinterpret_cast<const float4 *>(x),
-                       n / 4, part, reinterpret_cast<uint2 *>(x16), x_slot, zero_slot);
+                       n / 4, part, reinterpret_cast<uint2 *>(x16), x_slot, hp_parts);
     return hipGetLastError();
 }
 
-hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *slot,
-                               const uint32_t *off, const uint32_t *count, uint32_t experts, uint32_t inter,
-                               uint32_t sh_row0, uint32_t sh_rows) {
+hipError_t rmda_launch_hp_cast(hipStream_t s, const float *hp32, uint16_t *hp16, const uint32_t *hp_parts,
+                               uint32_t *slot, const uint32_t *off, const uint32_t *count, uint32_t experts,
+                               uint32_t inter, uint32_t sh_row0, uint32_t sh_rows) {
     hipLaunchKernelGGL(hp_cast_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<const float4 *>(hp32),
-                       reinterpret_cast<uint2 *>(hp16), slot, off, count, experts, inter, sh_row0, sh_rows);
+                       reinterpret_cast<uint2 *>(hp16), hp_parts, slot, off, count, experts, inter, sh_row0,
+                       sh_rows);
     return hipGetLastError();
 }

@@ -272,6 +272,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     const uint32_t b_row_off = A_BYTES + (wn * 64 + fr) * (BK * 2);
     const uint32_t rq = 4 * fq;
     floatx4_t acc[4][4];
+    float hmax_run = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU| over its tasks
     uint32_t c_row0 = 0;
     uint32_t c_rows = 0;
     uint32_t c_nt = 0;
@@ -346,7 +347,6 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                 // same output columns
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
                 const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
-                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -358,13 +358,10 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }
-                }
-                if (SC) {
-                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -443,6 +440,9 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
         load_frags(cbuf, fa0, fb0);
         cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
         compute(fa0, fb0);
+    }
+    if (SC && MODE == RMDA_GEMM_SWIGLU) {
+        rmda_wave_amax(g.hp_amax, hmax_run);
     }
 }
 
@@ -720,6 +720,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     const uint32_t b_row_off = A_BYTES + (wn * 64 + fr) * (BK * 2);
     const uint32_t rq = 4 * fq;
     floatx4_t acc[4][4];
+    float hmax_run = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU| over its tasks
     uint32_t c_row0 = 0;
     uint32_t c_rows = 0;
     uint32_t c_nt = 0;
@@ -815,7 +816,6 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             } else {
                 const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
                 const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
-                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -827,13 +827,10 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }
-                }
-                if (SC) {
-                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -842,6 +839,9 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
             ks = 0;
             kc += 1;
         }
+    }
+    if (SC && MODE == RMDA_GEMM_SWIGLU) {
+        rmda_wave_amax(g.hp_amax, hmax_run);
     }
 }
 
@@ -1037,6 +1037,7 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
     const uint32_t b_off = (wn * 64 + fr) * (BK * 2) + (fq ^ swz<BK>(fr)) * 16;
     const uint32_t rq = 4 * fq;
     floatx4_t acc[4][4];
+    float hmax_run = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU| over its tasks
     uint32_t c_row0 = 0;
     uint32_t c_rows = 0;
     uint32_t c_nt = 0;
@@ -1102,7 +1103,6 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
             uint16_t *O = reinterpret_cast<uint16_t *>(g.out);
             const uint32_t slab = c_nt * (BN / SLAB) + (wn * 64) / SLAB;
             const uint32_t colbase = slab * (SLAB / 2) + (((wn * 64) % SLAB) / 64) * 32;
-            float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
             for (int i = 0; i < 4; i += 1) {
 #pragma unroll
@@ -1114,13 +1114,10 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
                             const float gt = acc[i][j][v] * xinv;
                             const float up = acc[i][j + 2][v] * xinv;
                             const float h = rmda_swiglu_fast(gt, up);
-                            swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
+                            swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                         }
                     }
                 }
-            }
-            if (SC) {
-                rmda_wave_amax(g.hp_amax, hmax);
             }
         }
         ks += 1;
@@ -1128,6 +1125,9 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
             ks = 0;
             kc += 1;
         }
+    }
+    if (SC) {
+        rmda_wave_amax(g.hp_amax, hmax_run);
     }
 }
 

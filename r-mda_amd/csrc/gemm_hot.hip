@@ -158,6 +158,7 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     const uint32_t b_off = A_BYTES + (wn * 64 + fr) * (HK * 2) + (fq ^ swz<HK>(fr)) * 16;
     const uint32_t rq = 4 * fq;
     floatx4_t acc[8][4];
+    float hmax_run = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU| over its tasks
     half8_t fa[8], fb[4];
     uint32_t c_row0 = 0;
     uint32_t c_rows = 0;
@@ -227,7 +228,6 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
                 // slab rows wn*64 .. +64 are 32 gate rows then the 32 matching
                 // up rows: blocks j (gate) and j + 2 (up) share output columns
                 const uint32_t colbase = c_nt * (HN / 2) + wn * 32;
-                float hmax = 0.0f;  // slot-scaled mode: this lane's largest |SwiGLU|
 #pragma unroll
                 for (int i = 0; i < 8; i += 1) {
 #pragma unroll
@@ -239,13 +239,10 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax);
+                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }
-                }
-                if (SC) {
-                    rmda_wave_amax(g.hp_amax, hmax);
                 }
             }
         }
@@ -278,6 +275,9 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
             load_frags(cbuf);
             cbuf = cbuf + 1 == STAGES ? 0 : cbuf + 1;
             compute();
+        }
+        if (SC && MODE == RMDA_GEMM_SWIGLU) {
+            rmda_wave_amax(g.hp_amax, hmax_run);
         }
         return;
     }
@@ -322,6 +322,9 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
         if (!g1 || gs + 1 < nstage) {
             __builtin_amdgcn_s_barrier();
         }
+    }
+    if (SC && MODE == RMDA_GEMM_SWIGLU) {
+        rmda_wave_amax(g.hp_amax, hmax_run);
     }
 }
 

@@ -130,7 +130,8 @@ typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
 // One SwiGLU output of the gate_up epilogue: fp16 into hp, or in the
 // slot-scaled mode (SC, a template parameter of every GEMM kernel, so the
 // default epilogue carries no test of it) fp32 into hp32 with its magnitude
-// into the lane's running maximum (rmda_wave_amax merges it after the tile).
+// into the lane's running maximum over its tasks (rmda_wave_amax merges it at
+// the kernel's end).
 // Both tiles store through this, so they stay bitwise equal in either mode.
 template <bool SC>
 __device__ __forceinline__ void swiglu_store(const rmda_gemm_args_t &g, uint16_t *O, size_t hi, float h,
