@@ -54,6 +54,10 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t A_STEP = MODE == RMDA_GEMM_F16 ? RMDA_HP_ROWS * HK : HK;  // hp is in 16 x 32 blocks
     static_assert(RPI == RMDA_HP_ROWS, "one A instruction = one hp block");
     static_assert(STAGES >= 2 && STAGES <= 5 && STAGES * STAGE_BYTES <= 160 * 1024, "pipeline depth");
+    // All of the kernel's LDS is this one array: with a second __shared__
+    // array the compiler cannot tell the fragment reads from the DMA targets
+    // and waits for every outstanding DMA (s_waitcnt vmcnt(0)) before each
+    // stage's reads, which halves the tile's speed.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
 
     const uint32_t tid = threadIdx.x;
