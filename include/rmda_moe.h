@@ -187,12 +187,14 @@ int rmda_moe_set_tile_policy(rmda_moe_ctx_t *ctx, int policy);
 /* Route inside the rank launch for calls of more than one rank block of
  * 1024 (token, expert) pairs, up to 65536 pairs: the
  * launches before gate_up are then the router and one rank launch, in which
- * one workgroup per 8 tokens selects the top-k as moe_route does
+ * one workgroup per 16 tokens selects the top-k as moe_route does
  * (shader/moe_route.comp:20-61, dispatched at src/qwen.c:799-811) and the
  * workgroups that finish last rank the pairs, after a device-scope
  * release/acquire ticket.  Off by default: slower on MI355X (config 3 layer
- * 308.0 -> 310-312 us, config 5 815 -> 818-821 us), because that hand-off
- * costs more than the kernel boundary it replaces.  Calls of one rank block
+ * 292.5 -> 293.9 us, config 5 794.2 -> 797.8 us), because every rank block
+ * then reads all pairs' experts, written on other XCDs, through device-scope
+ * loads, which costs more than the kernel boundary it replaces (route + rank
+ * 9.7 us, the routed rank 14.2 us at config 3).  Calls of one rank block
  * (decode sizes) always route in the rank launch.  Every setting gives
  * bitwise the same results. */
 int rmda_moe_set_route_in_rank(rmda_moe_ctx_t *ctx, int on);

@@ -728,6 +728,22 @@ hipError_t rmda_launch_scan(hipStream_t s, const uint32_t *count, uint32_t *off,
     return hipGetLastError();
 }
 
+// the routed rank launch: one block per NTR / 64 rows routes; the last
+// blocks to finish rank (rank_kernel, NV > 0)
+template <uint32_t NTR>
+void launch_routed(hipStream_t s, const rmda_rank_args_t *a, uint32_t nv) {
+    const dim3 g1((a->route_rows + NTR / RMDA_WAVE - 1) / (NTR / RMDA_WAVE)), b1(NTR);
+    if (nv <= 1) {
+        hipLaunchKernelGGL((rank_kernel<NTR, 1>), g1, b1, 0, s, *a);
+    } else if (nv <= 2) {
+        hipLaunchKernelGGL((rank_kernel<NTR, 2>), g1, b1, 0, s, *a);
+    } else if (nv <= 4) {
+        hipLaunchKernelGGL((rank_kernel<NTR, 4>), g1, b1, 0, s, *a);
+    } else {
+        hipLaunchKernelGGL((rank_kernel<NTR, RMDA_MAX_EXPERTS / RMDA_WAVE>), g1, b1, 0, s, *a);
+    }
+}
+
 hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     uint32_t nb = (a->npairs + RMDA_RANK_BLOCK - 1) / RMDA_RANK_BLOCK;
     if (nb == 0) {
@@ -739,13 +755,14 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
     // config 5, 20 blocks over 512 experts: rank 15.5 -> 10.2 us; config 3
     // 7.6 -> 7.35 us; one block is 0.15 us slower with 1024)
     if (a->route_proj != nullptr) {
-        // top-k folded in: one block per 8 rows routes, the last nb to finish
-        // rank (8-wave blocks: decode rank 7.45-7.65 -> 7.16-7.19 us against
-        // 4-wave ones; 16-wave ones took 8.8-9.1, their last block then
-        // routing as well as ranking the most).  Several rank blocks need
+        // top-k folded in: one block per 8 rows (16 with several rank
+        // blocks) routes, the last nb to finish rank (one rank block, decode:
+        // 8-wave blocks took 7.16-7.19 us, 4-wave ones 7.45-7.65 and 16-wave
+        // ones 8.8-9.1, their last block then routing as well as ranking the
+        // most; several: 16-wave blocks, config 3 rank 15.4 -> 14.5 us,
+        // config 5 25.4 -> 23.0 us against 8-wave ones).  Several rank blocks need
         // count_all (each counts every pair, so none waits for another's
         // totals) and write the permutation themselves.
-        constexpr uint32_t NTR = 512;
         const bool multi_ok = a->count_all != 0 && a->slot != nullptr && a->npairs <= RMDA_RANK_ALL_MAX &&
                               (reinterpret_cast<uintptr_t>(a->idx) & 15u) == 0;
         if ((nb != 1 && !multi_ok) || a->experts > RMDA_MAX_EXPERTS || a->topk == 0 || a->done == nullptr ||
@@ -753,15 +770,12 @@ hipError_t rmda_launch_rank(hipStream_t s, const rmda_rank_args_t *a) {
             return hipErrorInvalidValue;
         }
         const uint32_t nv = (a->experts + RMDA_WAVE - 1) / RMDA_WAVE;
-        const dim3 g1((a->route_rows + NTR / RMDA_WAVE - 1) / (NTR / RMDA_WAVE)), b1(NTR);
-        if (nv <= 1) {
-            hipLaunchKernelGGL((rank_kernel<NTR, 1>), g1, b1, 0, s, *a);
-        } else if (nv <= 2) {
-            hipLaunchKernelGGL((rank_kernel<NTR, 2>), g1, b1, 0, s, *a);
-        } else if (nv <= 4) {
-            hipLaunchKernelGGL((rank_kernel<NTR, 4>), g1, b1, 0, s, *a);
+        if (nb == 1) {
+            launch_routed<512>(s, a, nv);
         } else {
-            hipLaunchKernelGGL((rank_kernel<NTR, RMDA_MAX_EXPERTS / RMDA_WAVE>), g1, b1, 0, s, *a);
+            // several rank blocks rank faster with one thread per pair, as
+            // the unrouted launch does
+            launch_routed<1024>(s, a, nv);
         }
         return hipGetLastError();
     }
