@@ -407,8 +407,8 @@ typedef struct rmda_moe_ws_layout_t {
 
 size_t rmda_moe_workspace_bytes(const rmda_moe_shape_t *shape);
 /* Workspace of rmda_moe_layer with args->x32 set: the scaled fp16 copy of x
- * and the fp32 SwiGLU output / expert rows on top of the above (config 3:
- * 112.9 MB against 104.5 MB). */
+ * and the fp32 SwiGLU output / expert rows in place of the fp16 expert rows
+ * (config 3: 188.1 MB against 104.7 MB). */
 size_t rmda_moe_workspace_bytes_x32(const rmda_moe_shape_t *shape);
 int rmda_moe_workspace_layout(const rmda_moe_shape_t *shape, rmda_moe_ws_layout_t *out);
 
@@ -435,7 +435,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape,
  * loaded and held until the process ends.  Shapes whose
  * rmda_moe_workspace_bytes (with x32: rmda_moe_workspace_bytes_x32) exceeds
  * it fail with RMDA_ERR_CAPACITY (config 3, T=2048 x d=2048 x 128 experts
- * top-8, needs 104.5 MB).  The call allocates
+ * top-8, needs 104.7 MB, and 188.1 MB with x32).  The call allocates
  * nothing and enqueues only kernels (the rank ticket it needs zeroed is
  * cleared by the router kernel).  Every call on a device shares that device's
  * array and leaves its contents behind, so calls that overlap on one device

@@ -215,13 +215,13 @@ class Context:
         self._check(self.L.rmda_moe_layer(self.h, ctypes.byref(s), ctypes.byref(args)))
 
     def layer_static(self, shape, x, w_router, bias, out, packed=None, w_gate_up=None, w_down=None,
-                     w_sh_gate_up=None, w_sh_down=None, h=None, inj=None, inj_stride=0, inj_off=0, hc=0):
+                     w_sh_gate_up=None, w_sh_down=None, h=None, inj=None, inj_stride=0, inj_off=0, hc=0, x32=None):
         """rmda_moe_layer_static: the layer on the library's static scratch
-        (no workspace argument, nothing allocated)."""
+        (no workspace argument, nothing allocated); x32 as in layer()."""
         s = shape_struct(shape)
         args = LayerArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(w_gate_up), _ptr(w_down),
                          _ptr(w_sh_gate_up), _ptr(w_sh_down), _ptr(out), None, 0, _ptr(packed), _ptr(h), _ptr(inj),
-                         inj_stride, inj_off, hc)
+                         inj_stride, inj_off, hc, _ptr(x32))
         self._check(self.L.rmda_moe_layer_static(self.h, ctypes.byref(s), ctypes.byref(args)))
 
     def pack_weights(self, shape, w_router, w_gate_up, w_down, w_sh_gate_up=None, w_sh_down=None, bf16=False,

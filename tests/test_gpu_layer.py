@@ -415,6 +415,52 @@ def test_layer_fp32_activations_of_fp16_values(ctx):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
+def test_layer_fp32_activations_reused_workspace_and_tiles(ctx):
+    """The slot-scaled mode keeps no state between calls: a call with
+    activations of 1e-6 on a workspace that a 1e6 call used first (its hp
+    absmax words then hold 1e6-scale values) is bitwise the same call on a
+    fresh workspace; and the compute tile (every expert hot), the streaming
+    tile and both launched (AUTO) give bitwise the same outputs."""
+    cfg = dict(name="x32_reuse", rows=600, d=512, experts=16, topk=4, inter=256, shared=256, skew=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=21)
+    shape = inp["shape"]
+    T, d = shape["rows"], shape["d"]
+    g = torch.Generator(device="cuda").manual_seed(21)
+    x_big = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * 1e6
+    x_small = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * 1e-6
+    packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+    nbytes = api.workspace_bytes_x32(shape)
+
+    def run(x32, ws, policy, hot_rows):
+        ctx.set_tile_policy(policy)
+        ctx.set_hot_rows(hot_rows)
+        h = torch.zeros(T, 1, d, dtype=torch.float32, device="cuda")
+        inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+        out = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
+        ctx.layer(shape, None, inp["w_router"], inp["bias"], None, None, None, None, out, ws, packed=packed, h=h,
+                  inj=inj, inj_stride=1, inj_off=0, hc=1, x32=x32)
+        ctx.sync()
+        return h, out
+
+    try:
+        fresh = torch.full((nbytes,), 255, dtype=torch.uint8, device="cuda")
+        ref_h, ref_out = run(x_small, fresh, api.Context.TILE_STREAM, 256)
+        assert torch.isfinite(ref_h).all() and ref_h.abs().max() > 0
+        ws = torch.full((nbytes,), 255, dtype=torch.uint8, device="cuda")
+        big_h, _ = run(x_big, ws, api.Context.TILE_STREAM, 256)
+        assert big_h.abs().max() > 1e3 * ref_h.abs().max()
+        for policy, hot_rows in ((api.Context.TILE_STREAM, 256), (api.Context.TILE_HOT, 1),
+                                 (api.Context.TILE_AUTO, 1), (api.Context.TILE_AUTO, 0)):
+            h, out = run(x_small, ws, policy, hot_rows)
+            print("x32 reuse: policy %d hot rows %d" % (policy, hot_rows), flush=True)
+            assert torch.equal(h.view(torch.int32), ref_h.view(torch.int32)), (policy, hot_rows)
+            assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16)), (policy, hot_rows)
+    finally:
+        ctx.set_tile_policy(api.Context.TILE_ADAPTIVE)
+        ctx.set_hot_rows(256)
+
+
 def test_layer_fp32_activations_rejections(ctx):
     """x and x32 together, and a workspace sized for the fp16 mode, are
     rejected before anything is enqueued."""

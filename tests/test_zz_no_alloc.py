@@ -44,13 +44,50 @@ def test_static_layer_two_calls():
     torch.cuda.set_device(0)
     ctx = api.Context(0)
     try:
-        # config 3 (104.5 MB of workspace, the largest benchmark shape that
+        # config 3 (104.7 MB of workspace, the largest benchmark shape that
         # fits), then a smaller ragged call on the scratch it left behind
         run_pair(ctx, configs.CONFIGS[3], seed=0)
         run_pair(ctx, dict(configs.CONFIGS[1], rows=203, name="ragged"), seed=5)
         # HF-layout weights and the shared expert, then config 4 (the hot tile)
         run_pair(ctx, configs.CONFIGS[5] | dict(rows=1024, name="fine_shared_1k"), seed=1, packed_too=False)
         run_pair(ctx, configs.CONFIGS[4], seed=0)
+    finally:
+        ctx.close()
+
+
+def test_static_layer_fp32_activations():
+    """The static layer with fp32 activations (the slot-scaled mode) against
+    rmda_moe_layer with a caller workspace, bitwise, on two calls in a row:
+    config 3's shape at 1024 tokens (103.4 MB of workspace in this mode;
+    2048 tokens need 188.1 MB, more than the scratch) with activations of
+    1e4, then a smaller call of 1e-4 on the scratch the first one left
+    behind."""
+    torch.cuda.set_device(0)
+    ctx = api.Context(0)
+    try:
+        for cfg, seed, mag in ((dict(configs.CONFIGS[3], rows=1024, name="prefill_1k"), 0, 1e4),
+                               (dict(configs.CONFIGS[1], rows=203, name="ragged"), 5, 1e-4)):
+            print("static layer x32 %s mag %g" % (cfg["name"], mag), flush=True)
+            inp = inputs.make_inputs(ctx, cfg, seed=seed)
+            shape = inp["shape"]
+            assert api.workspace_bytes_x32(shape) <= STATIC_WS_BYTES
+            x32 = inp["x"].float() * mag
+            packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                                      inp["w_sh_down"])
+            ws = torch.full((api.workspace_bytes_x32(shape),), 255, dtype=torch.uint8, device="cuda")
+            T, d = shape["rows"], shape["d"]
+            hs = [torch.zeros(T, 1, d, dtype=torch.float32, device="cuda") for _ in range(2)]
+            inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+            ref = torch.full((T, d), float("nan"), dtype=torch.float16, device="cuda")
+            got = torch.full_like(ref, float("nan"))
+            ctx.layer(shape, None, inp["w_router"], inp["bias"], None, None, None, None, ref, ws, packed=packed,
+                      h=hs[0], inj=inj, inj_stride=1, inj_off=0, hc=1, x32=x32)
+            ctx.layer_static(shape, None, inp["w_router"], inp["bias"], got, packed=packed, h=hs[1], inj=inj,
+                             inj_stride=1, inj_off=0, hc=1, x32=x32)
+            ctx.sync()
+            assert torch.isfinite(hs[0]).all()
+            assert torch.equal(hs[1].view(torch.int32), hs[0].view(torch.int32)), "static-scratch layer differs"
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     finally:
         ctx.close()
 
