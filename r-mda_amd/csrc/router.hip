@@ -460,8 +460,8 @@ __global__ __launch_bounds__(MF_NW * RMDA_WAVE) void router_mf_kernel(
 // four steps of v_mfma_f32_16x16x4f32 on its four token tiles.  The weight
 // float4 of chunk q for the next step is loaded as soon as this step's has
 // been used, a full step (8 chunks) ahead.
-constexpr uint32_t RW_TOK = 64;            // tokens per workgroup
-constexpr uint32_t RW_TT = RW_TOK / 16;    // token tiles per wave
+// TT token tiles of 16 per wave and workgroup: 4 (64 tokens) by default, 2
+// (32 tokens) when 64-token workgroups would be too few
 constexpr uint32_t RW_NW = 8;              // waves per workgroup
 constexpr uint32_t RW_COL = 16 * RW_NW;    // columns per workgroup
 constexpr uint32_t RW_NT = RW_NW * RMDA_WAVE;
@@ -473,6 +473,7 @@ __device__ __forceinline__ void rw_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+template <uint32_t TT>
 __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__restrict__ x16,
                                                             const float *__restrict__ w,
                                                             const float *__restrict__ bias,
@@ -480,7 +481,8 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
                                                             uint32_t cols, uint32_t cpad, uint32_t stride,
                                                             uint32_t nbias, uint32_t *zero_words, uint32_t n_zero,
                                                             const uint32_t *xscale) {
-    __shared__ float4 xs[2][NQ][RW_TT][RMDA_WAVE];
+    constexpr uint32_t TOK = 16 * TT;
+    __shared__ float4 xs[2][NQ][TT][RMDA_WAVE];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % RMDA_WAVE;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid / RMDA_WAVE);
@@ -491,7 +493,7 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
     }
     const uint32_t L = d / NQ;
     const uint32_t nsub = L / 16;  // d % 128 == 0 is a launch condition
-    const uint32_t t0 = blockIdx.x * RW_TOK;
+    const uint32_t t0 = blockIdx.x * TOK;
     const uint32_t kk = lane / 16;
     const uint32_t c = blockIdx.y * RW_COL + wv * 16 + lane % 16;  // < cpad: the grid covers whole 128-column blocks
     // weight float4 of chunk q, step s: steps 0..3 of lane (kk, column c)
@@ -499,34 +501,36 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
     const size_t wq = (size_t)nsub * cpad * 16;  // one chunk further
     const size_t ws = (size_t)cpad * 16;         // one 16-k step further
 
-    // staging: thread tid takes the 8-element halves p = tid and tid + RW_NT
-    // of the step's 8 x 64 x 2 halves: chunk p / 128, token (p % 128) / 2,
-    // half p % 2 (k 8h .. 8h+7 of the step)
-    const uint16_t *xsrc[2];
-    uint32_t xdst[2];  // float index in xs[0] of the token's float4 for kk = 0, plus 2h
+    // staging: thread tid takes the 8-element halves p = tid + r * RW_NT
+    // (r < NH) of the step's 8 x TOK x 2 halves: chunk p / (2 TOK), token
+    // (p % (2 TOK)) / 2, half p % 2 (k 8h .. 8h+7 of the step)
+    constexpr uint32_t NH = NQ * TOK * 2 / RW_NT;
+    static_assert(NH * RW_NT == NQ * TOK * 2, "whole halves per thread");
+    const uint16_t *xsrc[NH];
+    uint32_t xdst[NH];  // float index in xs[0] of the token's float4 for kk = 0, plus 2h
 #pragma unroll
-    for (uint32_t r = 0; r < 2; r += 1) {
+    for (uint32_t r = 0; r < NH; r += 1) {
         const uint32_t pc = tid + r * RW_NT;
-        const uint32_t q = pc / 128;
-        const uint32_t tok = (pc % 128) / 2;
+        const uint32_t q = pc / (2 * TOK);
+        const uint32_t tok = (pc % (2 * TOK)) / 2;
         const uint32_t h = pc % 2;
         const uint32_t row = t0 + tok < rows ? t0 + tok : rows - 1;  // rows past the matrix: never stored
         xsrc[r] = x16 + (size_t)row * d + q * L + 8 * h;
-        xdst[r] = ((q * RW_TT + tok / 16) * RMDA_WAVE + tok % 16) * 4 + 2 * h;
+        xdst[r] = ((q * TT + tok / 16) * RMDA_WAVE + tok % 16) * 4 + 2 * h;
     }
     float *const xsf = reinterpret_cast<float *>(&xs[0][0][0][0]);
-    constexpr uint32_t XBUF = NQ * RW_TT * RMDA_WAVE * 4;  // floats per buffer
-    uint4 xv[2];
+    constexpr uint32_t XBUF = NQ * TT * RMDA_WAVE * 4;  // floats per buffer
+    uint4 xv[NH];
     auto load_x = [&](uint32_t s) {
 #pragma unroll
-        for (uint32_t r = 0; r < 2; r += 1) {
+        for (uint32_t r = 0; r < NH; r += 1) {
             xv[r] = *reinterpret_cast<const uint4 *>(xsrc[r] + (size_t)s * 16);
         }
     };
     // element o of a half is k offset 8h + o: kk = o % 4, step 2h + o / 4
     auto store_x = [&](uint32_t buf) {
 #pragma unroll
-        for (uint32_t r = 0; r < 2; r += 1) {
+        for (uint32_t r = 0; r < NH; r += 1) {
             const uint32_t u[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
 #pragma unroll
             for (uint32_t k4 = 0; k4 < 4; k4 += 1) {
@@ -540,9 +544,9 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
         }
     };
 
-    rmda_f32x4 acc[RW_TT][NQ];
+    rmda_f32x4 acc[TT][NQ];
 #pragma unroll
-    for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+    for (uint32_t tt = 0; tt < TT; tt += 1) {
 #pragma unroll
         for (uint32_t q = 0; q < NQ; q += 1) {
             acc[tt][q] = rmda_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -575,27 +579,27 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
         const float4 *xa = &xs[buf][0][0][lane];
 #pragma unroll
         for (uint32_t q = 0; q < NQ; q += 1) {
-            float4 a[RW_TT];
+            float4 a[TT];
 #pragma unroll
-            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
-                a[tt] = xa[(q * RW_TT + tt) * RMDA_WAVE];
+            for (uint32_t tt = 0; tt < TT; tt += 1) {
+                a[tt] = xa[(q * TT + tt) * RMDA_WAVE];
             }
             const float4 bq = wcur[q];
             wnext[q] = *reinterpret_cast<const float4 *>(wc + q * wq + (size_t)sn * ws);
 #pragma unroll
-            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+            for (uint32_t tt = 0; tt < TT; tt += 1) {
                 acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].x, bq.x, acc[tt][q], 0, 0, 0);
             }
 #pragma unroll
-            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+            for (uint32_t tt = 0; tt < TT; tt += 1) {
                 acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].y, bq.y, acc[tt][q], 0, 0, 0);
             }
 #pragma unroll
-            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+            for (uint32_t tt = 0; tt < TT; tt += 1) {
                 acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].z, bq.z, acc[tt][q], 0, 0, 0);
             }
 #pragma unroll
-            for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+            for (uint32_t tt = 0; tt < TT; tt += 1) {
                 acc[tt][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[tt].w, bq.w, acc[tt][q], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -616,7 +620,7 @@ __global__ __launch_bounds__(RW_NT) void router_wide_kernel(const uint16_t *__re
     const float bv = bias != nullptr && c < nbias ? bias[c] : 0.0f;
     const float xinv = rmda_slot_inv(xscale);
 #pragma unroll
-    for (uint32_t tt = 0; tt < RW_TT; tt += 1) {
+    for (uint32_t tt = 0; tt < TT; tt += 1) {
 #pragma unroll
         for (uint32_t v = 0; v < 4; v += 1) {
             float sum = acc[tt][0][v];
@@ -682,11 +686,20 @@ void launch_mf(hipStream_t s, uint32_t rows, uint32_t cols, bool w_packed, const
         // the wide tile takes whole 128-column blocks when they give the GPU
         // enough workgroups; the columns past them (the shared-expert gate)
         // go to the tile below
+        // (64-token workgroups, or 32-token ones when those are too few: the
+        // teacher's T = 2048 x 512 experts, 71.5 us on the 32 x 32 tile ->
+        // 53.9 us)
         const uint32_t nbw = cols / RW_COL;
-        if (nbw > 0 && (rows + RW_TOK - 1) / RW_TOK * nbw >= RW_MIN_WGS) {
-            const dim3 grid((rows + RW_TOK - 1) / RW_TOK, nbw);
-            hipLaunchKernelGGL(router_wide_kernel, grid, dim3(RW_NT), 0, s, x16, w, bias, proj, rows, d, cols, cpad,
-                               stride, nbias, zero_words, n_zero, xscale);
+        const bool w64 = (rows + 63) / 64 * nbw >= RW_MIN_WGS;
+        const bool w32 = !w64 && (rows + 31) / 32 * nbw >= RW_MIN_WGS;
+        if (nbw > 0 && (w64 || w32)) {
+            if (w64) {
+                hipLaunchKernelGGL(router_wide_kernel<4>, dim3((rows + 63) / 64, nbw), dim3(RW_NT), 0, s, x16, w,
+                                   bias, proj, rows, d, cols, cpad, stride, nbias, zero_words, n_zero, xscale);
+            } else {
+                hipLaunchKernelGGL(router_wide_kernel<2>, dim3((rows + 31) / 32, nbw), dim3(RW_NT), 0, s, x16, w,
+                                   bias, proj, rows, d, cols, cpad, stride, nbias, zero_words, n_zero, xscale);
+            }
             col0 = nbw * RW_COL;
             zero_words = nullptr;
             if (col0 == cols) {

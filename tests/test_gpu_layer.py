@@ -111,6 +111,9 @@ TEACHER = dict(name="teacher", rows=256, d=2560, experts=512, topk=10, inter=640
     dict(name="wide_router_shared", rows=3100, d=256, experts=512, topk=4, inter=128, shared=128, skew=False),
     # 65 x 3 wide workgroups, no remainder columns, 6 k steps per router chunk
     dict(name="wide_router_e384", rows=4100, d=768, experts=384, topk=6, inter=128, shared=0, skew=False),
+    # 32-token wide workgroups (64-token ones would be 32 x 4 < 192): 63 x 4,
+    # the last token block ragged, the shared gate's column by the small tile
+    dict(name="wide32_router_shared", rows=1999, d=512, experts=512, topk=4, inter=128, shared=128, skew=False),
     TEACHER,
 ], ids=lambda c: c["name"])
 def test_layer_more_shapes(ctx, cfg):
