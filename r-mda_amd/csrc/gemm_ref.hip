@@ -17,6 +17,14 @@
 //     LDS with global_load_lds_dwordx4 through a 3-stage ring of 48 KiB; a
 //     row's 16-byte chunk c sits at slot c ^ ((r >> 1) & 7), which keeps the
 //     16-lane fragment reads free of bank conflicts.
+//   * A task's K loop starts at step 5e mod (k/64) for expert e and wraps
+//     round.  With every task starting at k = 0, all CUs would read the same
+//     128 bytes of each 4 KiB weight row at once; those addresses agree in
+//     their low 12 bits and crowd into few HBM channels (rows 4 KiB apart
+//     streamed in step: 4.3 TB/s, against 5.4-5.9 with staggered starts,
+//     measured on MI355X; gate_up at config 3: 234 -> 213 us).  The start
+//     depends on the expert only, so every variant sums each output in the
+//     same order, and an expert's row tiles still read its weights together.
 //   * 8 MFMA waves = 2 (M, 64 rows) x 4 (N, 64 columns),
 //     v_mfma_f32_16x16x32_f16, fp32 accumulate; they also write C.  Four more
 //     waves issue all of the DMA (4 A and 8 B instructions per stage each) and
@@ -145,11 +153,13 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
         const uint32_t lch = lane % CH;
         const uint16_t *a_src[A_PER];
         const uint16_t *b_src[B_PER];
+        uint32_t k_rot = 0;  // the task's first K step
         auto setup = [&](uint32_t q) __attribute__((always_inline)) {
             uint32_t nt;
             const uint32_t ci = sched.item(q, nt);
-            const uint32_t t = tl[ci];
+            const uint32_t t = __builtin_amdgcn_readfirstlane(tl[ci]);
             const uint32_t grp = g.tiles[t];
+            k_rot = grp * 5 % steps;
             const uint16_t *wg = g.w + (size_t)grp * g.n_w * g.k;
             // LIVE: padding rows load the tile's first row instead (a cache
             // hit, not an HBM read); their results are not stored
@@ -180,15 +190,16 @@ __global__ __launch_bounds__(768) void ref_mm_kernel(rmda_gemm_args_t g) {
                 setup(i_task);
             }
             uint8_t *base = smem + buf * STAGE_BYTES;
+            const uint32_t kk = i_s + k_rot < steps ? i_s + k_rot : i_s + k_rot - steps;
 #pragma unroll
             for (uint32_t j = 0; j < A_PER; j += 1) {
-                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + i_s * RK),
+                __builtin_amdgcn_global_load_lds((const void *)(a_src[j] + kk * RK),
                                                  (lds_void_t *)(base + (dw * A_PER + j) * RPI * (RK * 2)), 16, 0, 0);
             }
 #pragma unroll
             for (uint32_t j = 0; j < B_PER; j += 1) {
                 __builtin_amdgcn_global_load_lds(
-                    (const void *)(b_src[j] + i_s * RK),
+                    (const void *)(b_src[j] + kk * RK),
                     (lds_void_t *)(base + A_BYTES + (dw * B_PER + j) * RPI * (RK * 2)), 16, 0, 0);
             }
             i_s += 1;
