@@ -29,7 +29,8 @@ Prints ONE JSON line.  Besides the driver's fields it carries
                 each tile forced for the whole call;
   teacher       (config-3 runs) the reference teacher's own MoE shape (d 2560,
                 512 experts, top-10, width 640 + shared) at 2048 tokens: the
-                fused layer and the reference-structured recording;
+                fused layer with fp16 and with fp32 (slot-scaled)
+                activations, and the reference-structured recording;
   fp32_activations  (config-3 runs) config 3 through the slot-scaled
                 fp32-activation input;
   alternating_layers  (config-3 runs) configs 3 and 4 alternating on one
@@ -476,10 +477,14 @@ def measure_teacher(ctx, torch, steps=50, warmup=20):
     width 640 with a shared expert; src/qwen.c:11-37) at the training batch
     of 2048 tokens: the fused layer on packed weights, and the reference's
     recording (rmda_qwen_moe_rec: 128-row segments, slot-scaled casts, fp32
-    rows, hyper-connection streams out) on the HF-layout weights."""
+    rows, hyper-connection streams out) on the HF-layout weights; the fused
+    layer also with fp32 activations (slot-scaled)."""
     from rmda_moe import api, configs, inputs
     cfg = configs.TEACHER
     res = {"fused": measure_config(ctx, torch, cfg, steps=steps, warmup=warmup)}
+    # the path qwen.c's fused forwarder takes: the chunk's fp32 activations
+    # through the reference's slot-scaled casts
+    res["fused_fp32_activations"] = measure_config(ctx, torch, cfg, steps=steps, warmup=warmup, x32=True)
     inp = inputs.make_inputs(ctx, cfg, seed=0)
     s = inp["shape"]
     T, d = s["rows"], s["d"]
