@@ -358,7 +358,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
+                                swiglu_store<SC, true>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }
@@ -827,7 +827,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
+                                swiglu_store<SC, true>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }
@@ -1114,7 +1114,7 @@ __global__ __launch_bounds__(1024) void gemm4_kernel(rmda_gemm_args_t g) {
                             const float gt = acc[i][j][v] * xinv;
                             const float up = acc[i][j + 2][v] * xinv;
                             const float h = rmda_swiglu_fast(gt, up);
-                            swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
+                            swiglu_store<SC, true>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                         }
                     }
                 }

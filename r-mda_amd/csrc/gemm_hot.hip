@@ -243,7 +243,7 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
                                 const float gt = acc[i][j][v] * xinv;
                                 const float up = acc[i][j + 2][v] * xinv;
                                 const float h = rmda_swiglu_fast(gt, up);
-                                swiglu_store<SC>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
+                                swiglu_store<SC, false>(g, O, rmda_hp_index(c_row0 + rr, colbase + j * 16 + fr, g.ldo), h, hmax_run);
                             }
                         }
                     }

@@ -133,12 +133,24 @@ typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
 // into the lane's running maximum over its tasks (rmda_wave_amax merges it at
 // the kernel's end).
 // Both tiles store through this, so they stay bitwise equal in either mode.
-template <bool SC>
+// NT: a non-temporal store, which keeps the outputs from displacing the
+// gathered activation rows that the item's other N tiles read from L2 next.
+// The streaming tile takes it (measured on MI355X: gate_up at config 3
+// 150.4 -> 139.1 us, config 5 413.8 -> 383.9 us, the teacher's shape 603 ->
+// 586 us); the compute tile does not (config 4: 109.3 -> 112.6 us, and its
+// down GEMM then reads hp from HBM).
+template <bool SC, bool NT>
 __device__ __forceinline__ void swiglu_store(const rmda_gemm_args_t &g, uint16_t *O, size_t hi, float h,
                                              float &hmax) {
     if constexpr (SC) {
-        g.hp32[hi] = h;
+        if constexpr (NT) {
+            __builtin_nontemporal_store(h, &g.hp32[hi]);
+        } else {
+            g.hp32[hi] = h;
+        }
         hmax = fmaxf(hmax, fabsf(h));
+    } else if constexpr (NT) {
+        __builtin_nontemporal_store(rmda_f2h(h), &O[hi]);
     } else {
         O[hi] = rmda_f2h(h);
     }
