@@ -496,13 +496,30 @@ __device__ __forceinline__ uint2 cast4(const float4 &v, float sc) {
 // absmax.comp over x, one part per block (no slot word to clear first)
 __global__ __launch_bounds__(256) void x_absmax_kernel(const float4 *__restrict__ x, size_t n4,
                                                        uint32_t *__restrict__ part) {
+    // four loads in flight per thread (the maximum does not depend on the order)
+    constexpr uint32_t U = 4;
+    const size_t st = (size_t)gridDim.x * 256;
     float m = 0.0f;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-        const float4 v = x[i];
+    auto take = [&](const float4 &v) {
         m = fmaxf(m, fabsf(v.x));
         m = fmaxf(m, fabsf(v.y));
         m = fmaxf(m, fabsf(v.z));
         m = fmaxf(m, fabsf(v.w));
+    };
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + (U - 1) * st < n4; i += U * st) {
+        float4 v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            v[u] = x[i + u * st];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            take(v[u]);
+        }
+    }
+    for (; i < n4; i += st) {
+        take(x[i]);
     }
     const uint32_t r = block_max_bits(m);
     if (threadIdx.x == 0) {
@@ -537,7 +554,21 @@ __global__ __launch_bounds__(256) void x_cast_kernel(const float4 *__restrict__ 
         }
     }
     const float sc = amax_scale(amax);
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    constexpr uint32_t U = 4;
+    const size_t st = (size_t)gridDim.x * 256;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + (U - 1) * st < n4; i += U * st) {
+        float4 v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            v[u] = x[i + u * st];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u += 1) {
+            x16[i + u * st] = cast4(v[u], sc);
+        }
+    }
+    for (; i < n4; i += st) {
         x16[i] = cast4(x[i], sc);
     }
 }
