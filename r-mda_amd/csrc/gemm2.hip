@@ -48,11 +48,18 @@
 //     pair of K steps.
 //   * gemm3_kernel (packed weights, the default): four more waves issue all
 //     of the DMA and nothing else, so a stage's loads leave right after the
-//     stage barrier instead of queueing behind MFMAs; for gate_up a second
-//     barrier after the fragment reads frees a buffer before its MFMAs run,
-//     so all STAGES buffers are in flight.  Measured at config 3 against
+//     stage barrier instead of queueing behind MFMAs; a second barrier
+//     after the fragment reads frees a buffer before its MFMAs run, so all
+//     STAGES buffers are in flight.  Measured at config 3 against
 //     gemm2_kernel on the same boxes: gate_up 175.3 -> 172.6 us, down
-//     106.1 -> 104.9 us (the second barrier helps gate_up, not down).
+//     106.1 -> 104.9 us.  The second barrier was first kept for gate_up
+//     only; with the non-temporal SwiGLU stores in place, giving it to the
+//     down GEMM as well takes the layer at config 3 from 303 to 297 us and
+//     from 289 to 286-288 us on two boxes, at config 5 from 789 to 775 and
+//     756 to 750 us, from fp32 activations at config 3 from 336 to 327-331
+//     us; configs 2 and 4 are unchanged and the teacher's shape from fp32
+//     activations 0.4% slower.  Most of the gain shows in the next call's
+//     gate_up, not in down itself (at 512 experts down is 2% slower).
 #include "common.h"
 #include "gemm_sched.h"
 
@@ -1203,7 +1210,7 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
         }
         if (c.spec == 7 && MODE == RMDA_GEMM_SWIGLU && a->k % 64 == 0) {
             hipLaunchKernelGGL((gemm4_kernel<5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
-        } else if (c.spec == 5 || ((c.spec == 6 || c.spec == 7) && MODE == RMDA_GEMM_SWIGLU)) {
+        } else if (c.spec != 4) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true, false, true>), grid, dim3(16 * RMDA_WAVE), 0, s,
                                *a);
         } else {
@@ -1225,7 +1232,7 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
                                s, *a);
             return hipGetLastError();
         }
-        if (c.spec == 5 || ((c.spec == 6 || c.spec == 7) && MODE == RMDA_GEMM_SWIGLU)) {
+        if (c.spec != 4) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
         } else {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
@@ -1248,7 +1255,7 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
 
 // Variant 0 is the default: the fastest configuration measured on MI355X at
 // the benchmark shapes (packed weights run the dedicated-issue kernel, with
-// the second per-stage barrier for gate_up only, and the layer switches
+// the second per-stage barrier for both GEMMs, and the layer switches
 // gate_up to the activation-ring kernel when experts average 32 rows or
 // more; HF-layout weights always run gemm2_kernel).  The others are kept for
 // measurement.  LDS per workgroup =
@@ -1259,7 +1266,7 @@ rmda_gemm2_cfg_t rmda_gemm2_variant(int variant) {
     case 2: return {256, 32, 4, 0, 2, 0};  // the same with 4 stages
     case 3: return {256, 32, 5, 0, 0, 0};  // the same without the non-temporal weight hint
     case 4: return {256, 32, 5, 0, 2, 4};  // dedicated issue waves, one barrier per stage
-    case 5: return {256, 32, 5, 0, 2, 5};  // dedicated issue waves, two barriers per stage
+    case 5: return {256, 32, 5, 0, 2, 5};  // the default without the activation-ring switch
     case 7: return {256, 32, 5, 0, 2, 7};  // gate_up with its activation rows in a two-K-step ring
     default: return {256, 32, 5, 0, 2, 6};
     }
