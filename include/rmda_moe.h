@@ -590,8 +590,9 @@ int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n,
  * reference's sequence stage by stage (128-row segments, scaled fp16 casts,
  * fp32 GEMM outputs); rmda_moe_layer is the fused fast path.
  * Differences, as for the stage entry points: the router is the fp32
- * rmda_moe_router (its p holds the experts' logits and, with a shared
- * expert, the shared gate in column `experts`; the shared gate/up
+ * rmda_moe_router on the slot-scaled cast of x, each chunk sum multiplied
+ * by the slot's inverse scale (its p holds the experts' logits and, with a
+ * shared expert, the shared gate in column `experts`; the shared gate/up
  * projections come from w_sh_gate_up through rmda_moe_mm instead of from
  * further p columns).  All functions are enqueue-only, return a status and
  * leave it sticky in ctx; nothing is allocated. */

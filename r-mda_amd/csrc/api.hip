@@ -1695,7 +1695,7 @@ int rmda_moe_fill_normal_f32(rmda_moe_ctx_t *ctx, float *dst, size_t n, uint64_t
 namespace {
 
 struct ShimPlan {
-    size_t x16, a16, p, idx, wt, count, off, fill, tiles, slot, xp, g, hp, hp16, ye;
+    size_t a16, p, idx, wt, count, off, fill, tiles, slot, xp, g, hp, hp16, ye;
     size_t gs, hs, hs16, sh, tiles1, amax, wr, total;
     uint32_t ps, rows_pad, mrows;
 };
@@ -1726,7 +1726,6 @@ ShimPlan plan_shim(const rmda_qwen_moe_t *q) {
         o = align256(o + bytes);
         return at;
     };
-    p.x16 = take((size_t)T * d * 2);
     p.a16 = take((size_t)p.rows_pad * d * 2);
     p.p = take((size_t)T * p.ps * 4);
     p.idx = take((size_t)T * K * 4);
@@ -1939,14 +1938,14 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
     // mda_qwen_slots_begin (src/qwen.c:500-503)
     q->n_slots = 0;
     rc = hip_check(c, rmda_launch_zero(c->stream, amax, RMDA_QWEN_MAX_SLOTS, 0), "moe_rec slot fill");
-    // A0: x cast with a slot for the GEMMs; the fp32 router reads x as fp16
+    // A0: x cast with a slot (src/qwen.c:844); the fp32 router reads the same
+    // cast and multiplies each chunk sum by the slot's inverse scale, which
+    // for fp16-range activations gives the logits of x itself bit for bit
+    // and keeps activations outside that range (subnormal or above 65504 as
+    // fp16) at full precision
     uint32_t sx = RMDA_NO_SLOT;
     if (rc == RMDA_OK) {
         rc = shim_cast(q, p, x, scr<uint16_t>(q, p.a16), rows * d, &sx);
-    }
-    if (rc == RMDA_OK) {
-        const rmda_pc_cast_t pc{rows * d, RMDA_NO_SLOT};
-        rc = rmda_cast_f16(c, &pc, x, scr<uint16_t>(q, p.x16), amax);
     }
     // the router projection on the router matrix repacked into the order the
     // router kernel streams (3.6 us for 128 x 2048 at config 3; the HF-layout
@@ -1958,8 +1957,8 @@ int rmda_qwen_moe_rec(rmda_qwen_moe_t *q, const float *x, const float *inj, floa
     }
     if (rc == RMDA_OK) {
         rc = hip_check(c,
-                       rmda_launch_router(c->stream, scr<uint16_t>(q, p.x16), scr<float>(q, p.wr), 1, nullptr,
-                                          scr<float>(q, p.p), rows, d, p.ps, p.ps, 0, nullptr, 0, nullptr),
+                       rmda_launch_router(c->stream, scr<uint16_t>(q, p.a16), scr<float>(q, p.wr), 1, nullptr,
+                                          scr<float>(q, p.p), rows, d, p.ps, p.ps, 0, nullptr, 0, nullptr, amax + sx),
                        "moe_rec router");
     }
     // A1-A3 (xp's padding rows are not zero-filled: the GEMMs, SwiGLU,

@@ -9,7 +9,8 @@ way tests/test_gpu_layer.py checks the benchmark configurations:
 On packed weights the compute tile (every expert hot), the streaming tile
 and both enqueued (AUTO) must then give bitwise the same output.  Every
 third shape also runs with fp32 activations of a random magnitude through
-the slot-scaled mode, against the oracle's fp32-activation mode.
+the slot-scaled mode, against the oracle's fp32-activation mode, and every
+second one through the qwen.c recording (rmda_qwen_moe_rec) the same way.
 """
 import numpy as np
 import pytest
@@ -111,6 +112,51 @@ def test_sweep_fp32_activations(ctx, cfg):
     assert np.array_equal(u32(views["idx"]), ref["idx"]), "expert indices"
     assert np.array_equal(u32(views["count"]), ref["count"]), "per-expert counts"
     assert np.array_equal(u32(views["slot"]), ref["slot"]), "permutation"
+    y = h[:, 0, :].cpu().numpy().astype(np.float64)
+    want = ref["out"].astype(np.float64)
+    assert np.isfinite(y).all()
+    scale = np.abs(want).max()
+    err = np.abs(y - want).max()
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want) if scale > 0 else 0.0
+    print("  max|y| %.3g rel-L2 %.3g max-abs %.3g" % (scale, rel, err), flush=True)
+    assert rel <= 1e-3 and err <= 1e-2 * scale, (rel, err)
+
+
+@pytest.mark.parametrize("cfg", SHAPES[1::2], ids=lambda c: c["name"])
+def test_sweep_recording(ctx, cfg):
+    """The qwen.c recording (rmda_qwen_moe_rec: 128-row segments, slot-scaled
+    fp16 casts, fp32 GEMM outputs) on every second sweep shape, from fp32
+    activations of a random magnitude, into one hyper-connection stream
+    (h += y * 2 * sigmoid(0) = y), against the oracle in the reference's
+    mode: logits, routing, 128-row offsets and the permutation bit-exact, y
+    within rel-L2 1e-3 and max-abs 1e-2 of its largest magnitude.  The
+    recording takes no router bias, so skewed shapes route uniformly here."""
+    seed = int(cfg["name"][5:]) + 200
+    mag = float(np.random.default_rng(seed).choice([1e-4, 1.0, 1e4]))
+    print("rec %s mag %g" % (cfg["name"], mag), flush=True)
+    inp = inputs.make_inputs(ctx, cfg, seed=seed)
+    shape = inp["shape"]
+    T, d = shape["rows"], shape["d"]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x32 = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * mag
+    q = api.QwenMoe(ctx, shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                    inp["w_sh_down"], hc=1, hc_rank=0, inj_stride=1)
+    q.scratch.fill_(255)
+    h = torch.zeros(T, 1, d, dtype=torch.float32, device="cuda")
+    inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+    q.moe_rec(x32, T, inj=inj, h=h)
+    ctx.sync()
+    host = inputs.to_host(inp)
+    host["x"] = None
+    host["bias"] = None
+    host["x32"] = x32.cpu().numpy()
+    ref = orc.layer(host, tile=128, x_scale=1, hp_scale=1, threads=16)
+    v = q.views(T)
+    assert np.array_equal(v["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(v["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(v["count"]), ref["count"]), "per-expert counts"
+    assert np.array_equal(u32(v["off"]), ref["off"]), "128-row segment offsets"
+    assert np.array_equal(u32(v["slot"]), ref["slot"]), "permutation"
     y = h[:, 0, :].cpu().numpy().astype(np.float64)
     want = ref["out"].astype(np.float64)
     assert np.isfinite(y).all()
