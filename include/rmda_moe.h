@@ -320,7 +320,7 @@ int rmda_qwen_bf16(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_bf16_t *pc, uint32_t 
  * fp32 arithmetic in one fixed order that the CPU oracle replays exactly:
  * d is cut into 8 contiguous chunks; each chunk is a sequential fmaf chain
  * from 0; the chunk sums are added left to right; then the bias.
- * Requires d % 32 == 0, stride >= cols, cols <= 1024. */
+ * Requires d % 128 == 0 and 1 <= cols <= stride, cols <= 65536. */
 typedef struct rmda_moe_router_t {
     uint32_t rows;
     uint32_t d;
@@ -331,6 +331,17 @@ typedef struct rmda_moe_router_t {
 
 int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc,
                     const uint16_t *x16, const float *w, const float *bias, float *proj);
+
+/* The router on a slot-scaled cast, as src/qwen.c:844-845 feeds it
+ * (mda_qwen_mm(q, sx, ...) on the cast mda_qwen_cast made with slot sx):
+ * x16 is x cast by rmda_cast_f16 with slot `slot` of amax, and each chunk
+ * sum is multiplied by the inverse of that slot's power-of-two scale before
+ * the bias is added.  For activations in fp16's normal range the logits
+ * equal rmda_moe_router's on the unscaled cast bit for bit; outside it
+ * (subnormal, or beyond 65504) they keep the precision of the scaled cast.
+ * slot == RMDA_NO_SLOT is rmda_moe_router.  Same requirements. */
+int rmda_moe_router_slot(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint16_t *x16, uint32_t slot,
+                         const uint32_t *amax, const float *w, const float *bias, float *proj);
 
 /* ---- fused MoE layer (replaces mda_qwen_moe_rec, src/qwen.c:838-907) ---- */
 

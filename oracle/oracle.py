@@ -110,6 +110,7 @@ def lib():
         L.orc_fill_normal_f16.argtypes = [_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float]
         L.orc_fill_normal_f32.argtypes = [_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float]
         L.orc_router.argtypes = [_p, _p, _p, _p, _p, ctypes.c_int]
+        L.orc_router_scaled.argtypes = [_p, _p, _p, _p, ctypes.c_float, _p, ctypes.c_int]
         L.orc_moe_route.argtypes = [_p, _p, _p, _p, _p]
         L.orc_moe_scan.argtypes = [_p, _p, _p, _p, _u32]
         L.orc_moe_scatter.argtypes = [_p] * 7
@@ -176,17 +177,22 @@ def h2f(a):
 
 # ---- per-stage -----------------------------------------------------------
 
-def router(x16, w, bias=None, nbias=None, stride=None, threads=None):
-    """proj = x16 . w^T (+ bias) in the canonical order.  x16 uint16 [T,d], w f32 [cols,d]."""
+def router(x16, w, bias=None, nbias=None, stride=None, threads=None, post=None):
+    """proj = x16 . w^T (+ bias) in the canonical order.  x16 uint16 [T,d], w f32 [cols,d].
+    With `post`, every chunk sum is multiplied by it before the bias
+    (orc_router_scaled: the router on a slot-scaled x16 with 1/scale)."""
     T, d = x16.shape
     cols = w.shape[0]
     stride = cols if stride is None else stride
     nbias = (0 if bias is None else bias.shape[0]) if nbias is None else nbias
     proj = np.zeros((T, stride), np.float32)
     pc = RouterPC(T, d, cols, stride, nbias)
-    lib().orc_router(_ref(pc), _ptr(np.ascontiguousarray(x16)), _ptr(np.ascontiguousarray(w)),
-                     _ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)),
-                     _ptr(proj), _nthreads(threads))
+    args = (_ptr(np.ascontiguousarray(x16)), _ptr(np.ascontiguousarray(w)),
+            _ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)))
+    if post is None:
+        lib().orc_router(_ref(pc), *args, _ptr(proj), _nthreads(threads))
+    else:
+        lib().orc_router_scaled(_ref(pc), *args, post, _ptr(proj), _nthreads(threads))
     return proj
 
 

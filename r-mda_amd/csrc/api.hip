@@ -899,12 +899,21 @@ int rmda_qwen_bf16(rmda_moe_ctx_t *ctx, const rmda_pc_qwen_bf16_t *pc, uint32_t 
 
 int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint16_t *x16, const float *w,
                     const float *bias, float *proj) {
+    return rmda_moe_router_slot(ctx, pc, x16, RMDA_NO_SLOT, nullptr, w, bias, proj);
+}
+
+int rmda_moe_router_slot(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint16_t *x16, uint32_t slot,
+                         const uint32_t *amax, const float *w, const float *bias, float *proj) {
     int rc = enter(ctx);
     if (rc != RMDA_OK) {
         return rc;
     }
-    if (pc == nullptr || x16 == nullptr || w == nullptr || proj == nullptr) {
+    if (pc == nullptr || x16 == nullptr || w == nullptr || proj == nullptr ||
+        (slot != RMDA_NO_SLOT && amax == nullptr)) {
         return fail(ctx, RMDA_ERR_ARG, "rmda_moe_router: null argument");
+    }
+    if (!aligned(amax, 4)) {
+        return fail(ctx, RMDA_ERR_ARG, "rmda_moe_router: amax not 4-byte aligned");
     }
     if (pc->d == 0 || pc->d % 128 != 0 || pc->cols == 0 || pc->cols > 65536 || pc->stride < pc->cols) {
         return fail(ctx, RMDA_ERR_SHAPE, "rmda_moe_router: d=%u cols=%u stride=%u (need d %% 128 == 0, "
@@ -914,8 +923,10 @@ int rmda_moe_router(rmda_moe_ctx_t *ctx, const rmda_moe_router_t *pc, const uint
     if (pc->rows == 0) {
         return RMDA_OK;
     }
-    return hip_check(ctx, rmda_launch_router(ctx->stream, x16, w, 0, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
-                                             bias != nullptr ? pc->nbias : 0, nullptr, 0, nullptr),
+    return hip_check(ctx,
+                     rmda_launch_router(ctx->stream, x16, w, 0, bias, proj, pc->rows, pc->d, pc->cols, pc->stride,
+                                        bias != nullptr ? pc->nbias : 0, nullptr, 0, nullptr,
+                                        slot != RMDA_NO_SLOT ? amax + slot : nullptr),
                      "router");
 }
 

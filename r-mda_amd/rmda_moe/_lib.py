@@ -142,6 +142,7 @@ SIGNATURES = {
     "rmda_cast_f16": (ctypes.c_int, [_p, _p, _p, _p, _p]),
     "rmda_qwen_bf16": (ctypes.c_int, [_p, _p, _p]),
     "rmda_moe_router": (ctypes.c_int, [_p, _p, _p, _p, _p, _p]),
+    "rmda_moe_router_slot": (ctypes.c_int, [_p, _p, _p, _u32, _p, _p, _p, _p]),
     "rmda_moe_workspace_bytes": (ctypes.c_size_t, [_p]),
     "rmda_moe_workspace_bytes_x32": (ctypes.c_size_t, [_p]),
     "rmda_moe_workspace_layout": (ctypes.c_int, [_p, _p]),

@@ -195,10 +195,16 @@ class Context:
         pc = Bf16PC(n)
         self._check(self.L.rmda_qwen_bf16(self.h, ctypes.byref(pc), _ptr(w)))
 
-    def router(self, rows, d, cols, stride, nbias, x16, w, bias, proj):
+    def router(self, rows, d, cols, stride, nbias, x16, w, bias, proj, slot=None, amax=None):
+        """rmda_moe_router; with `slot` (and the slot words `amax`) x16 is a
+        slot-scaled cast and rmda_moe_router_slot divides the scale out."""
         pc = RouterPC(rows, d, cols, stride, nbias)
-        self._check(self.L.rmda_moe_router(self.h, ctypes.byref(pc), _ptr(x16), _ptr(w), _ptr(bias),
-                                           _ptr(proj)))
+        if slot is None:
+            self._check(self.L.rmda_moe_router(self.h, ctypes.byref(pc), _ptr(x16), _ptr(w), _ptr(bias),
+                                               _ptr(proj)))
+        else:
+            self._check(self.L.rmda_moe_router_slot(self.h, ctypes.byref(pc), _ptr(x16), slot, _ptr(amax), _ptr(w),
+                                                    _ptr(bias), _ptr(proj)))
 
     # ---- fused layer ----
 

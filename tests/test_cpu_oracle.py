@@ -129,6 +129,27 @@ def test_router_thread_count_does_not_change_bits():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_router_scaled_equals_unscaled_for_fp16_inputs():
+    """orc_router_scaled on x cast with a power-of-two slot scale, with
+    1/scale as `post`: scaling every product of a chain by a power of two
+    commutes with fp32 rounding (no subnormal or overflow here), so the logits
+    equal the unscaled router's bit for bit; a post that is not the inverse,
+    or one applied to the bias as well, is not."""
+    x = orc.fill_normal_f16(61 * 768, 1, 5, 1.0).reshape(61, 768)
+    w = orc.fill_normal_f32(24 * 768, 2, 5, 0.02).reshape(24, 768)
+    b = configs.skew_bias(24, 5)
+    xf = orc.h2f(x)
+    amax = orc.absmax(xf, np.zeros(16, np.uint32), 0)
+    xs = orc.cast_f16(xf, amax, 0).reshape(x.shape)
+    sc = orc.slot_scale(amax, 0)
+    assert sc != 1.0 and not np.array_equal(xs, x)
+    want = orc.router(x, w, b)
+    got = orc.router(xs, w, b, post=1.0 / sc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(orc.router(xs, w, b, post=2.0 / sc).view(np.uint32), want.view(np.uint32))
+    assert not np.allclose(orc.router(xs, w, b * np.float32(sc), post=1.0 / sc), want, rtol=1e-3)
+
+
 # ---------------------------------------------------------------- route (A1)
 
 def np_route(p, experts, topk):

@@ -194,24 +194,25 @@ def test_moe_rec_fused_swiglu_matches_mm_then_elem(ctx, cfg):
     assert bad.size == 0, "hp16 rows differ: %s" % bad[:8]
 
 
-def run_documented_stages(ctx, inp, buf, xp_garbage=None):
+def run_documented_stages(ctx, inp, buf, xp_garbage=None, x32=None, h=None):
     """One chunk through the stage entry points in the order INTEGRATION.md
     documents for a qwen.c that keeps its own recording (src/qwen.c:838-907):
-    slot words zeroed (:500-503), x cast with a slot for the GEMMs and
-    unscaled for the fp32 router, route, scan, xp zero-filled (:798), scatter,
-    gate_up, qwen_elem op 0, hp absmax + cast with a slot, down, combine.
-    `buf` holds every buffer and is reused across calls, as the reference's
-    scratch is."""
+    slot words zeroed (:500-503), x cast with a slot, the fp32 router on that
+    cast with the slot's scale divided out, route, scan, xp zero-filled
+    (:798), scatter, gate_up, qwen_elem op 0, hp absmax + cast with a slot,
+    down, combine.  x is the fp16 inputs' fp32 copy, or `x32`; with `h` the
+    combine adds y into one hyper-connection stream instead of writing
+    buf["out"].  `buf` holds every buffer and is reused across calls, as the
+    reference's scratch is."""
     s = inp["shape"]
     T, d, E, K, I = s["rows"], s["d"], s["experts"], s["topk"], s["inter"]
     mrows = (T * K + E * 127 + 127) // 128 * 128
-    x = inp["x"].float()
+    x = inp["x"].float() if x32 is None else x32
     amax = buf["amax"]
     amax.zero_()
     ctx.absmax(T * d, 0, x, amax)
     ctx.cast_f16(T * d, 0, x, buf["a16"], amax)
-    ctx.cast_f16(T * d, 0xFFFFFFFF, x, buf["x16"], amax)
-    ctx.router(T, d, E, E, 0, buf["x16"], inp["w_router"], None, buf["p"])
+    ctx.router(T, d, E, E, 0, buf["a16"], inp["w_router"], None, buf["p"], slot=0, amax=amax)
     ctx.route(T, E, K, E, buf["p"], buf["idx"], buf["wt"], buf["count"])
     ctx.scan(E, 128, buf["count"], buf["off"], buf["tiles"], mrows // 128)
     if xp_garbage is not None:
@@ -223,8 +224,28 @@ def run_documented_stages(ctx, inp, buf, xp_garbage=None):
     ctx.absmax(mrows * I, 1, buf["hp"], amax)
     ctx.cast_f16(mrows * I, 1, buf["hp"], buf["hp16"], amax)
     ctx.mm(mrows, d, I, 1, 0xFFFFFFFF, buf["hp16"], inp["w_down"], buf["ye"], amax, buf["tiles"])
-    ctx.combine_plain((T, d, K, E, E, 0, 0, 0), buf["wt"], buf["slot"], buf["ye"], buf["p"], None, buf["out"])
+    if h is None:
+        ctx.combine_plain((T, d, K, E, E, 0, 0, 0), buf["wt"], buf["slot"], buf["ye"], buf["p"], None, buf["out"])
+    else:
+        inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+        ctx.combine((T, d, K, E, E, 1, 0, 1), buf["wt"], buf["slot"], buf["ye"], buf["p"], None, inj, h)
     ctx.sync()
+
+
+def stage_buffers(cfg):
+    """The stage sequence's buffers: those the stages overwrite start as NaN /
+    all-ones; g, hp, hp16 and ye start at zero, so their only stale rows are
+    an earlier chunk's."""
+    T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
+    mrows = (T * K + E * 127 + 127) // 128 * 128
+    f32e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float32, device="cuda")
+    u32e = lambda n: torch.full((n,), -1, dtype=torch.int32, device="cuda")
+    f16e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float16, device="cuda")
+    z32 = lambda *shp: torch.zeros(shp, dtype=torch.float32, device="cuda")
+    return dict(amax=u32e(16), a16=f16e(T, d), p=f32e(T, E), idx=u32e(T * K), wt=f32e(T * K),
+                count=u32e(E), off=u32e(E), tiles=u32e(mrows // 128), xp=f16e(mrows, d), fill=u32e(E),
+                slot=u32e(T * K), g=z32(mrows, 2 * I), hp=z32(mrows, I),
+                hp16=torch.zeros(mrows, I, dtype=torch.float16, device="cuda"), ye=z32(mrows, d), out=f16e(T, d))
 
 
 def test_documented_stage_sequence_on_stale_scratch(ctx):
@@ -238,18 +259,7 @@ def test_documented_stage_sequence_on_stale_scratch(ctx):
     second chunk against the oracle in the reference's mode: routing
     bit-exact, output within tolerance."""
     cfg = dict(name="stages", rows=300, d=512, experts=16, topk=4, inter=256, shared=0, skew=False)
-    T, d, E, K, I = cfg["rows"], cfg["d"], cfg["experts"], cfg["topk"], cfg["inter"]
-    mrows = (T * K + E * 127 + 127) // 128 * 128
-    f32e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float32, device="cuda")
-    u32e = lambda n: torch.full((n,), -1, dtype=torch.int32, device="cuda")
-    f16e = lambda *shp: torch.full(shp, float("nan"), dtype=torch.float16, device="cuda")
-    # buffers the stages overwrite start as NaN / all-ones; g, hp, hp16 and ye
-    # start at zero, so their only stale rows are the first chunk's
-    z32 = lambda *shp: torch.zeros(shp, dtype=torch.float32, device="cuda")
-    buf = dict(amax=u32e(16), a16=f16e(T, d), x16=f16e(T, d), p=f32e(T, E), idx=u32e(T * K), wt=f32e(T * K),
-               count=u32e(E), off=u32e(E), tiles=u32e(mrows // 128), xp=f16e(mrows, d), fill=u32e(E),
-               slot=u32e(T * K), g=z32(mrows, 2 * I), hp=z32(mrows, I),
-               hp16=torch.zeros(mrows, I, dtype=torch.float16, device="cuda"), ye=z32(mrows, d), out=f16e(T, d))
+    buf = stage_buffers(cfg)
     prev = inputs.make_inputs(ctx, cfg, seed=8)
     run_documented_stages(ctx, prev, buf)
     inp = inputs.make_inputs(ctx, cfg, seed=9)
@@ -265,6 +275,40 @@ def test_documented_stage_sequence_on_stale_scratch(ctx):
     max_abs, rel = out_metrics(got, ref["out"])
     print("  max-abs %.3g rel-L2 %.3g" % (max_abs, rel), flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+@pytest.mark.parametrize("mag", [1e-4, 1e4])
+def test_documented_stage_sequence_fp32_activations(ctx, mag):
+    """The same stage sequence from fp32 activations outside fp16's normal
+    range (|x| around 1e-4, where fp16 is subnormal, or 1e4, where SwiGLU and
+    down outputs pass 65504), into one hyper-connection stream
+    (h += y * 2 * sigmoid(0) = y): routing bit-exact against the oracle's
+    fp32-activation mode, y within rel-L2 1e-3 and max-abs 1e-2 of its
+    largest magnitude."""
+    cfg = dict(name="stages", rows=300, d=512, experts=16, topk=4, inter=256, shared=0, skew=False)
+    T, d = cfg["rows"], cfg["d"]
+    buf = stage_buffers(cfg)
+    inp = inputs.make_inputs(ctx, cfg, seed=12)
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x32 = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * mag
+    h = torch.zeros(T, 1, d, dtype=torch.float32, device="cuda")
+    run_documented_stages(ctx, inp, buf, x32=x32, h=h)
+    host = inputs.to_host(inp)
+    host["x"] = None
+    host["x32"] = x32.cpu().numpy()
+    ref = orc.layer(host, tile=128, hp_scale=1, x_scale=1, threads=16)
+    assert np.array_equal(buf["p"].cpu().numpy().view(np.uint32), ref["proj"].view(np.uint32)), "router logits"
+    assert np.array_equal(u32(buf["idx"]), ref["idx"]), "expert indices"
+    assert np.array_equal(u32(buf["off"]), ref["off"]), "128-row segment offsets"
+    assert np.array_equal(u32(buf["slot"]), ref["slot"]), "permutation"
+    y = h[:, 0, :].cpu().numpy().astype(np.float64)
+    want = ref["out"].astype(np.float64)
+    assert np.isfinite(y).all()
+    scale = np.abs(want).max()
+    err = np.abs(y - want).max()
+    rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+    print("  mag %g max|y| %.3g rel-L2 %.3g max-abs %.3g" % (mag, scale, rel, err), flush=True)
+    assert rel <= 1e-3 and err <= 1e-2 * scale, (rel, err)
 
 
 def test_moe_rec_runs_twice_bitwise_and_chunks(ctx):

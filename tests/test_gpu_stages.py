@@ -72,6 +72,46 @@ def test_router_bitexact(ctx, rows, d, cols, stride, bias):
     assert np.all(got[:, cols:] == 7.0), "columns beyond cols must stay untouched"
 
 
+@pytest.mark.parametrize("mag,bias", [(1.0, True), (1e-5, False), (1e5, True)])
+def test_router_slot_bitexact(ctx, mag, bias):
+    """rmda_moe_router_slot on x cast with a slot (absmax + cast on the GPU)
+    against the oracle's scaled router with 1/scale, fp32 activations of
+    magnitude 1, 1e-5 (below fp16's normal range unscaled) and 1e5 (above
+    65504); for fp16-exact activations it equals rmda_moe_router on the
+    unscaled cast bit for bit."""
+    rows, d, cols = 77, 1024, 40
+    x32 = orc.fill_normal_f32(rows * d, configs.STREAM_X, 2, mag).reshape(rows, d)
+    w = orc.fill_normal_f32(cols * d, configs.STREAM_W_ROUTER, 2, 0.02).reshape(cols, d)
+    b = configs.skew_bias(cols, 2) if bias else None
+    nbias = cols if bias else 0
+    amax_h = orc.absmax(x32, np.zeros(16, np.uint32), 3)
+    xs = orc.cast_f16(x32, amax_h, 3).reshape(rows, d)
+    ref = orc.router(xs, w, b, nbias=nbias, post=1.0 / orc.slot_scale(amax_h, 3))
+    amax = torch.zeros(16, dtype=torch.int32, device="cuda")
+    a16 = torch.empty(rows, d, dtype=torch.float16, device="cuda")
+    xd, wd, bd = dev(x32), dev(w), None if b is None else dev(b)
+    ctx.absmax(rows * d, 3, xd, amax)
+    ctx.cast_f16(rows * d, 3, xd, a16, amax)
+    proj = torch.full((rows, cols), 7.0, dtype=torch.float32, device="cuda")
+    ctx.router(rows, d, cols, cols, nbias, a16, wd, bd, proj, slot=3, amax=amax)
+    ctx.sync()
+    assert np.array_equal(u16(a16), xs), "slot-scaled cast"
+    assert np.array_equal(proj.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    # fp16-exact activations: the same logits as the unscaled router
+    x16 = orc.f2h(x32 / np.float32(mag))
+    xe = dev(orc.h2f(x16))
+    amax.zero_()
+    ctx.absmax(rows * d, 3, xe, amax)
+    ctx.cast_f16(rows * d, 3, xe, a16, amax)
+    ctx.router(rows, d, cols, cols, nbias, a16, wd, bd, proj, slot=3, amax=amax)
+    plain = torch.full((rows, cols), 7.0, dtype=torch.float32, device="cuda")
+    ctx.router(rows, d, cols, cols, nbias, dev(x16), wd, bd, plain)
+    ctx.sync()
+    assert torch.equal(proj.view(torch.int32), plain.view(torch.int32))
+    assert np.array_equal(plain.cpu().numpy().view(np.uint32),
+                          orc.router(x16.reshape(rows, d), w, b, nbias=nbias).view(np.uint32))
+
+
 def test_router_special_values_bitexact(ctx):
     """The matrix-core router against fmaf on the values where an MFMA could
     differ from IEEE fused multiply-adds: subnormal products and partial sums
