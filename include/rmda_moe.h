@@ -387,8 +387,12 @@ typedef struct rmda_moe_layer_args_t {
      * fresh slot and x is cast to fp16 times 2^(141 - exponent(absmax))
      * (absmax.comp, cast_f16.comp), which the router and gate_up divide out;
      * the SwiGLU output is kept in fp32 and cast with a slot of its own
-     * (src/qwen.c:858-877), which down divides out; and down's rows stay
-     * fp32 up to the combine (src/qwen.c:878).  So activations far outside
+     * (src/qwen.c:858-877), which down divides out.  Down's rows (fp32 in
+     * the reference, src/qwen.c:878) stay fp32 up to the combine with
+     * HF-layout weights; with packed weights they are stored as fp16 times
+     * 2^-c, where 2^c exceeds the down weights' largest row sum of |w| (a
+     * bound the packing computes), so that no row can overflow, and the
+     * combine multiplies the power of two back.  So activations far outside
      * fp16's range (say 1e-6 or 1e6) route and multiply as in the reference.
      * For inputs that are fp16 values in fp16's normal range the routing is
      * bitwise that of x = those values.  Needs rmda_moe_workspace_bytes_x32
@@ -461,7 +465,10 @@ int rmda_moe_layer_static(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, co
 /* Bytes of one layer's packed weights: routed gate_up and down, the shared
  * expert's gate_up and down when shape->shared > 0 (fp16, same element
  * count as the HF tensors), then the fp32 router matrix (experts [+1 shared
- * gate] rows, padded to a multiple of 64).  0 when the shape is rejected. */
+ * gate] rows, padded to a multiple of 64), then 256 bytes whose first word
+ * is the down weights' largest row sum of |w| (fp32; rows whose sum is not
+ * finite left out), for the x32 mode's fp16 expert rows.  0 when the shape
+ * is rejected. */
 size_t rmda_moe_packed_bytes(const rmda_moe_shape_t *shape);
 
 /* Reorder one layer's HF-layout weights (w_router [E (+1)][d] fp32,

@@ -268,9 +268,10 @@ int check_shape(const rmda_moe_shape_t *s, char *why, size_t n) {
 
 // x32: the slot-scaled mode (fp32 activations): the scaled fp16 copy of x,
 // the absmax parts and two slot words, and a last region that holds first
-// the fp32 SwiGLU output (hp32) and then the fp32 expert rows (ye32), where
-// the default mode's is the fp16 ye.  Every offset but that of the last
-// region's end is the same in both modes.
+// the fp32 SwiGLU output (hp32) and then the expert rows (fp16 scaled by the
+// packed weights' bound, or fp32 ye32 for HF-layout weights), where the
+// default mode's is the fp16 ye.  Every offset but that of the last region's
+// end is the same in both modes.
 LayerPlan plan_layer(const rmda_moe_shape_t *s, bool x32 = false) {
     LayerPlan p{};
     const uint32_t T = s->rows;
@@ -324,7 +325,7 @@ LayerPlan plan_layer(const rmda_moe_shape_t *s, bool x32 = false) {
 // Offsets in 16-bit units.  Every region size is a multiple of 256 units
 // (d % 256 == 0), so each region starts 512-byte aligned.
 struct PackPlan {
-    size_t gate_up, down, sh_gate_up, sh_down, router, total;
+    size_t gate_up, down, sh_gate_up, sh_down, router, bound, total;
 };
 
 PackPlan plan_pack(const rmda_moe_shape_t *s) {
@@ -336,7 +337,9 @@ PackPlan plan_pack(const rmda_moe_shape_t *s) {
     p.sh_gate_up = p.down + (size_t)s->experts * d * s->inter;
     p.sh_down = p.sh_gate_up + (size_t)2 * s->shared * d;
     p.router = p.sh_down + d * s->shared;
-    p.total = p.router + 2 * d * rmda_router_cpad(cols);  // fp32
+    // the down weights' row-sum bound (one fp32 word; 256 bytes kept)
+    p.bound = p.router + 2 * d * rmda_router_cpad(cols);  // fp32 router rows before it
+    p.total = p.bound + 128;
     return p;
 }
 
@@ -1066,6 +1069,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     const uint16_t *w_sgu = packed != nullptr ? packed + pk.sh_gate_up : args->w_sh_gate_up;
     const uint16_t *w_sdn = packed != nullptr ? packed + pk.sh_down : args->w_sh_down;
     const float *w_rt = packed != nullptr ? reinterpret_cast<const float *>(packed + pk.router) : args->w_router;
+    const uint32_t *ye_bound = packed != nullptr ? reinterpret_cast<const uint32_t *>(packed + pk.bound) : nullptr;
 
     if (ctx->prof_on && ctx->prof_pending == RMDA_PROF_RING) {
         rc = prof_harvest(ctx);
@@ -1261,8 +1265,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.xscale = nullptr;
         g.hp32 = nullptr;
         g.hp_amax = nullptr;
+        // x32: fp16 expert rows scaled by the packed weights' row-sum bound;
+        // fp32 rows (the reference's ye) for HF-layout weights, which carry
+        // no bound
         g.yscale = hslot;
-        g.ye32 = x32 ? at<float>(ws, p.ye) : nullptr;  // fp32 expert rows (the reference's ye)
+        g.ye32 = x32 && packed == nullptr ? at<float>(ws, p.ye) : nullptr;
+        g.ye_bound = x32 && packed != nullptr ? ye_bound : nullptr;
         g.lda = I;
         g.w = w_dn;
         g.w_shared = w_sdn;
@@ -1294,7 +1302,7 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     }
     // A8/A9 combine (+ sigmoid-gated shared expert, + hyper-connection streams)
     const rmda_hc_t hcp{args->h, args->inj, args->inj_stride, args->inj_off, args->hc};
-    if (rc == RMDA_OK && x32) {
+    if (rc == RMDA_OK && x32 && packed == nullptr) {
         // fp32 expert rows: the reference's combine arithmetic
         // (shader/moe_combine.comp:26-40), fp16 out and/or the streams
         const float *ye32 = at<float>(ws, p.ye);
@@ -1310,7 +1318,8 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
     } else if (rc == RMDA_OK && !(fold_combine && tile_mode == 1u)) {
         rc = hip_check(ctx,
                        rmda_launch_combine16(s, wt, slot, ye, proj, p.ps, E, p.sh_row0, shape->shared > 0, args->out,
-                                             T, d, K, &hcp, fold_combine ? at<uint32_t>(ws, p.n_items_hot) : nullptr),
+                                             T, d, K, &hcp, fold_combine ? at<uint32_t>(ws, p.n_items_hot) : nullptr,
+                                             x32 ? hslot : nullptr, x32 ? ye_bound : nullptr),
                        "layer combine");
         if (rc == RMDA_OK) {
             rc = prof_mark(ctx, RMDA_STAGE_COMBINE + 1);
@@ -1395,6 +1404,20 @@ int pack_layer(rmda_moe_ctx_t *ctx, hipStream_t s, const rmda_moe_shape_t *shape
                        rmda_launch_router_pack(s, w_router, reinterpret_cast<float *>(packed + pk.router),
                                                E + (S > 0 ? 1u : 0u), d),
                        "pack router");
+    }
+    // the largest row sum of |w| over the packed down weights (routed and
+    // shared), which sizes the slot-scaled mode's fp16 expert rows; the rest
+    // of its 256 bytes is zero, so equal weights pack to equal buffers
+    uint32_t *bound = reinterpret_cast<uint32_t *>(packed + pk.bound);
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_zero(s, bound, 64, 0), "pack bound fill");
+    }
+    if (rc == RMDA_OK) {
+        rc = hip_check(ctx, rmda_launch_row_abs_max(s, packed + pk.down, E, d, I, bk, bound), "pack down bound");
+    }
+    if (rc == RMDA_OK && S > 0) {
+        rc = hip_check(ctx, rmda_launch_row_abs_max(s, packed + pk.sh_down, 1, d, S, bk, bound),
+                       "pack shared down bound");
     }
     return rc;
 }

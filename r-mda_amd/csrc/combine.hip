@@ -143,10 +143,15 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
                                                         uint32_t shared_row0, int has_shared,
                                                         uint16_t *__restrict__ out, uint32_t d,
                                                         uint32_t topk, rmda_hc_t hcp,
-                                                        const uint32_t *__restrict__ run_if) {
+                                                        const uint32_t *__restrict__ run_if,
+                                                        const uint32_t *__restrict__ yscale,
+                                                        const uint32_t *__restrict__ ybound) {
     if (run_if != nullptr && *run_if == 0) {
         return;  // the down GEMM folded the combine in
     }
+    // the slot-scaled mode's rows stand for y * f, f a power of two: taken
+    // into the weights, which gives the same products bit for bit
+    const float f = ybound != nullptr ? rmda_slot_inv(yscale) / rmda_ye_mul(ybound) : 1.0f;
     __shared__ uint32_t s_slot[RMDA_MAX_TOPK + 1];
     __shared__ float s_wt[RMDA_MAX_TOPK + 1];
     __shared__ float s_g[RMDA_MAX_HC];
@@ -154,11 +159,11 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
     const uint32_t tid = threadIdx.x;
     if (tid < topk) {
         s_slot[tid] = slot[(size_t)r * topk + tid];
-        s_wt[tid] = wt[(size_t)r * topk + tid];
+        s_wt[tid] = wt[(size_t)r * topk + tid] * f;
     }
     if (tid == 0 && has_shared) {
         s_slot[RMDA_MAX_TOPK] = shared_row0 + r;
-        s_wt[RMDA_MAX_TOPK] = sigmoidf(proj[(size_t)r * pstride + sg_off]);
+        s_wt[RMDA_MAX_TOPK] = sigmoidf(proj[(size_t)r * pstride + sg_off]) * f;
     }
     if (HC && tid < hcp.hc) {
         s_g[tid] = 2.0f * sigmoidf(hcp.inj[(size_t)r * hcp.inj_stride + hcp.inj_off + tid] / (float)hcp.hc);
@@ -227,16 +232,17 @@ hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t 
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
                                  uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
-                                 const rmda_hc_t *hc, const uint32_t *run_if) {
+                                 const rmda_hc_t *hc, const uint32_t *run_if, const uint32_t *yscale,
+                                 const uint32_t *ybound) {
     if (rows == 0) {
         return hipSuccess;
     }
     if (hc != nullptr && hc->h != nullptr) {
         hipLaunchKernelGGL(combine16_kernel<true>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride, sg_off,
-                           shared_row0, has_shared, out, d, topk, *hc, run_if);
+                           shared_row0, has_shared, out, d, topk, *hc, run_if, yscale, ybound);
     } else {
         hipLaunchKernelGGL(combine16_kernel<false>, dim3(rows), dim3(256), 0, s, wt, slot, y, proj, pstride,
-                           sg_off, shared_row0, has_shared, out, d, topk, rmda_hc_t{}, run_if);
+                           sg_off, shared_row0, has_shared, out, d, topk, rmda_hc_t{}, run_if, yscale, ybound);
     }
     return hipGetLastError();
 }

@@ -148,6 +148,23 @@ __device__ __forceinline__ float rmda_slot_inv(const uint32_t *amax) {
     return ldexpf(1.0f, (int)((u >> 23) & 0xffu) - 141);
 }
 
+// The slot-scaled mode's fp16 expert rows (packed weights).  bound is the
+// down weights' largest row sum of |w| (rows whose sum is not finite left
+// out), written when the weights are packed.  A SwiGLU output cast with its
+// slot is below 2^15 in magnitude, so every down product hp16 . w is below
+// 2^15 * bound; multiplied by rmda_ye_mul(bound) = 2^-c with 2^c > bound
+// (c >= 0) it stays below 2^15 and fits fp16 with fp16's relative
+// precision.  The combine multiplies it back by 2^c (exact: a power of two).
+// Read through the scalar cache, as rmda_slot_inv.
+__device__ __forceinline__ float rmda_ye_mul(const uint32_t *bound) {
+    const uint32_t u = *(const __attribute__((address_space(4))) uint32_t *)bound;
+    const uint32_t e = (u >> 23) & 0xffu;  // bound in [2^(e-127), 2^(e-126))
+    if (e < 127u || e == 0xffu) {
+        return 1.0f;  // below 1 (c = 0), or not finite
+    }
+    return ldexpf(1.0f, 126 - (int)e);
+}
+
 // The slot-scaled mode's SwiGLU absmax is gathered in RMDA_AMAX_PARTS partial
 // words, RMDA_AMAX_STRIDE words apart (one 128-byte line each), which the hp
 // cast folds, so that the GEMM waves' device-scope atomics spread over 64
@@ -484,14 +501,16 @@ struct rmda_gemm_args_t {
     // otherwise).  SWIGLU: g and u are multiplied by rmda_slot_inv(xscale)
     // before SiLU, and with hp32 set the SwiGLU output goes to hp32 as fp32
     // (same blocked index as the fp16 hp) instead of fp16 to out, and its
-    // absmax into the partial words hp_amax (RMDA_AMAX_BYTES, zeroed before).  F16: the output is multiplied by
-    // rmda_slot_inv(yscale), and with ye32 set it is stored to ye32 as fp32
-    // instead of fp16 to out.
+    // absmax into the partial words hp_amax (RMDA_AMAX_BYTES, zeroed before).  F16, one of: ye32 set, the
+    // output is multiplied by rmda_slot_inv(yscale) and stored to ye32 as
+    // fp32; ye_bound set (packed weights' row-sum bound word), it is
+    // multiplied by rmda_ye_mul(ye_bound) and stored as fp16 to out.
     const uint32_t *xscale;
     float *hp32;
     uint32_t *hp_amax;
     const uint32_t *yscale;
     float *ye32;
+    const uint32_t *ye_bound;
 };
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);
 // gemm_ref.hip: the F32 (reference matmul_f16_moe) contract on the
@@ -546,6 +565,11 @@ hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm
 // into the packed slab order of K step bk (SWIGLU: gate/up interleave).
 hipError_t rmda_launch_pack(hipStream_t s, const uint16_t *src, uint16_t *dst, uint32_t groups, uint32_t n_w,
                             uint32_t k, uint32_t inter, int swiglu, int bk, int bf16_in);
+// The largest row sum of |w| over `groups` packed (non-SwiGLU) matrices
+// [n_w][k] of K step bk, rows whose sum is not finite left out, atomicMax'ed
+// as float bits into *bound (which the caller zeroes first).
+hipError_t rmda_launch_row_abs_max(hipStream_t s, const uint16_t *packed, uint32_t groups, uint32_t n_w, uint32_t k,
+                                   int bk, uint32_t *bound);
 
 // combine.hip
 hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, const float *wt,
@@ -554,12 +578,15 @@ hipError_t rmda_launch_combine(hipStream_t s, const rmda_pc_moe_combine_t *pc, c
 // fused-layer combine: y fp16 rows, optional shared rows at shared_row0 + r.
 // run_if (or NULL): the kernel returns at once unless *run_if != 0 (the
 // layer passes the compute tile's item count when the down GEMM may have
-// folded the combine in)
+// folded the combine in).  yscale and ybound (or NULL): the slot-scaled
+// mode's fp16 rows, which stand for y * rmda_slot_inv(yscale) /
+// rmda_ye_mul(ybound); the weights are multiplied by that power of two.
 hipError_t rmda_launch_combine16(hipStream_t s, const float *wt, const uint32_t *slot,
                                  const uint16_t *y, const float *proj, uint32_t pstride,
                                  uint32_t sg_off, uint32_t shared_row0, int has_shared,
                                  uint16_t *out, uint32_t rows, uint32_t d, uint32_t topk,
-                                 const rmda_hc_t *hc, const uint32_t *run_if);
+                                 const rmda_hc_t *hc, const uint32_t *run_if, const uint32_t *yscale = nullptr,
+                                 const uint32_t *ybound = nullptr);
 
 // elem.hip
 hipError_t rmda_launch_elem(hipStream_t s, const rmda_pc_qwen_elem_t *pc, const float *a, float *y);

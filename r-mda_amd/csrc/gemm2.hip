@@ -134,7 +134,7 @@ __global__ __launch_bounds__(768) void gemm2_kernel(rmda_gemm_args_t g) {
     const_u32p items = (const_u32p)g.items;
     // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
     const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
-    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
+    const float yinv = down_mul<SC, MODE>(g);
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
@@ -596,7 +596,7 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     const_u32p items = (const_u32p)g.items;
     // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
     const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
-    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
+    const float yinv = down_mul<SC, MODE>(g);
     const uint32_t n_slabs = g.n_w / SLAB;
     const uint32_t ntiles = n_slabs / (BN / SLAB);
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
@@ -1176,6 +1176,45 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t *__restrict__ 
     }
 }
 
+// The largest row sum of |w| over `groups` packed F16-mode matrices [n_w][k]
+// (the down weights; one thread per weight row, its slab row's 64 bytes per
+// K step, so a wave reads whole lines), rows whose sum is not finite left
+// out, as float bits: a wave maximum, then one atomicMax per wave.
+template <int BK>
+__global__ __launch_bounds__(256) void row_abs_kernel(const uint16_t *__restrict__ packed, uint32_t groups,
+                                                      uint32_t n_w, uint32_t k, uint32_t *__restrict__ bound) {
+    constexpr uint32_t CH = BK / 8;
+    const uint32_t steps = k / BK;
+    const uint64_t rows = (uint64_t)groups * n_w;
+    const uint4 *units = reinterpret_cast<const uint4 *>(packed);
+    float m = 0.0f;
+    for (uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x; q < rows; q += (uint64_t)gridDim.x * 256) {
+        const uint64_t gi = q / n_w;
+        const uint32_t r = (uint32_t)(q % n_w);
+        // unit (gi, t, ks, n, p) = gi * n_w * k / 8 + ((t * steps + ks) * SLAB + n) * CH + p
+        const uint4 *u = units + gi * n_w * k / 8 + ((uint64_t)(r / SLAB) * steps * SLAB + r % SLAB) * CH;
+        float sum = 0.0f;
+        for (uint32_t ks = 0; ks < steps; ks += 1) {
+#pragma unroll
+            for (uint32_t p = 0; p < CH; p += 1) {
+                const uint4 v = u[(size_t)ks * SLAB * CH + p];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int i = 0; i < 4; i += 1) {
+                    sum += fabsf(rmda_h2f((uint16_t)(w4[i] & 0xffffu))) + fabsf(rmda_h2f((uint16_t)(w4[i] >> 16)));
+                }
+            }
+        }
+        if (sum <= 3.4028235e38f) {  // false for inf and NaN
+            m = fmaxf(m, sum);
+        }
+    }
+    const uint32_t b = rmda_wave_red_u32<true>(__builtin_bit_cast(uint32_t, m));
+    if (threadIdx.x % RMDA_WAVE == 0) {
+        atomicMax(bound, b);
+    }
+}
+
 template <int MODE, int BN, int BK, int STAGES, int BPOL, bool SC = false>
 hipError_t launch_cfg(hipStream_t s, const rmda_gemm_args_t *a, dim3 grid, bool packed) {
     if (packed) {
@@ -1196,10 +1235,10 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     const dim3 grid(wgs);
     // the slot-scaled mode (fp32 SwiGLU output or fp32 rows) has its own
     // instantiations, of the default configurations only
-    const bool sc = a->hp32 != nullptr || a->ye32 != nullptr;
+    const bool sc = a->hp32 != nullptr || a->ye32 != nullptr || a->ye_bound != nullptr;
     if (sc) {
-        if ((MODE == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) || (MODE == RMDA_GEMM_F16) != (a->ye32 != nullptr) ||
-            a->fc.cnt != nullptr) {
+        if ((MODE == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) ||
+            (MODE == RMDA_GEMM_F16) != ((a->ye32 != nullptr) != (a->ye_bound != nullptr)) || a->fc.cnt != nullptr) {
             return hipErrorInvalidValue;
         }
         if (c.spec == 0 || !packed) {
@@ -1283,6 +1322,24 @@ hipError_t rmda_launch_gemm2(hipStream_t s, const rmda_gemm_args_t *a, rmda_gemm
         return launch_mode<RMDA_GEMM_SWIGLU>(s, a, c, packed != 0);
     }
     return launch_mode<RMDA_GEMM_F16>(s, a, c, packed != 0);
+}
+
+hipError_t rmda_launch_row_abs_max(hipStream_t s, const uint16_t *packed, uint32_t groups, uint32_t n_w, uint32_t k,
+                                   int bk, uint32_t *bound) {
+    const uint64_t rows = (uint64_t)groups * n_w;
+    if (rows == 0) {
+        return hipSuccess;
+    }
+    if (n_w % SLAB != 0 || k % bk != 0 || (bk != 32 && bk != 64)) {
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid((uint32_t)std::min<uint64_t>((rows + 255) / 256, 4096));
+    if (bk == 64) {
+        hipLaunchKernelGGL(row_abs_kernel<64>, grid, dim3(256), 0, s, packed, groups, n_w, k, bound);
+    } else {
+        hipLaunchKernelGGL(row_abs_kernel<32>, grid, dim3(256), 0, s, packed, groups, n_w, k, bound);
+    }
+    return hipGetLastError();
 }
 
 hipError_t rmda_launch_pack(hipStream_t s, const uint16_t *src, uint16_t *dst, uint32_t groups, uint32_t n_w,

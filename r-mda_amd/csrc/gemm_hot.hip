@@ -69,7 +69,7 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     const_u32p items = (const_u32p)g.items;
     // the slot-scaled mode's inverse scales (1 otherwise, which changes no bits)
     const float xinv = SC && MODE == RMDA_GEMM_SWIGLU ? rmda_slot_inv(g.xscale) : 1.0f;
-    const float yinv = SC && MODE == RMDA_GEMM_F16 ? rmda_slot_inv(g.yscale) : 1.0f;
+    const float yinv = down_mul<SC, MODE>(g);
     const uint32_t ntiles = g.n_w / HN;
     const uint32_t n_items = g.n_items != nullptr ? *(const_u32p)g.n_items : g.max_items;
     const SCHED sched(n_items, ntiles);
@@ -373,10 +373,11 @@ hipError_t rmda_launch_gemm_hot(hipStream_t s, const rmda_gemm_args_t *a, uint32
         return hipSuccess;
     }
     const dim3 gr(grid >= 8 ? grid / 8 * 8 : 8);  // persistent: one workgroup per CU, whole XCDs
-    if (a->hp32 != nullptr || a->ye32 != nullptr) {
+    if (a->hp32 != nullptr || a->ye32 != nullptr || a->ye_bound != nullptr) {
         // the slot-scaled mode: the default configuration only
-        if ((a->mode == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) || (a->mode == RMDA_GEMM_F16) != (a->ye32 != nullptr) ||
-            stages != 4 || sched != 0) {
+        if ((a->mode == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) ||
+            (a->mode == RMDA_GEMM_F16) != ((a->ye32 != nullptr) != (a->ye_bound != nullptr)) || stages != 4 ||
+            sched != 0) {
             return hipErrorInvalidValue;
         }
         if (a->mode == RMDA_GEMM_SWIGLU) {

@@ -156,11 +156,22 @@ __device__ __forceinline__ void swiglu_store(const rmda_gemm_args_t &g, uint16_t
     }
 }
 
-// One output of the down epilogue, already multiplied by the inverse hp
-// slot scale: fp16 into ye, or fp32 into ye32 in the slot-scaled mode.
+// The down epilogue's multiplier: 1, or in the slot-scaled mode the inverse
+// hp slot scale (fp32 rows) or rmda_ye_mul of the packed weights' bound
+// (fp16 rows).
+template <bool SC, int MODE>
+__device__ __forceinline__ float down_mul(const rmda_gemm_args_t &g) {
+    if constexpr (SC && MODE == RMDA_GEMM_F16) {
+        return g.ye32 != nullptr ? rmda_slot_inv(g.yscale) : rmda_ye_mul(g.ye_bound);
+    }
+    return 1.0f;
+}
+
+// One output of the down epilogue, already multiplied by down_mul: fp16
+// into ye, or fp32 into ye32 in the slot-scaled mode's fp32-row variant.
 template <bool SC>
 __device__ __forceinline__ void down_store(const rmda_gemm_args_t &g, uint16_t *O, size_t i, float y) {
-    if constexpr (SC) {
+    if (SC && g.ye32 != nullptr) {
         g.ye32[i] = y;
     } else {
         O[i] = rmda_f2h(y);

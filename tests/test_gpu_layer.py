@@ -238,8 +238,13 @@ def test_pack_bf16_input_equals_fp16_of_converted(ctx):
     # the router matrix follows as [d/16][cols rounded up to 64][4][4] fp32, zero padded, bits
     # unchanged: element (k, c) at ((k/16)*cpad + c)*16 + (k%4)*4 + (k%16)/4
     cpad = (E + 63) // 64 * 64
-    rt = p_h[n_exp:].view(torch.float32).cpu().numpy()
+    rt = p_h[n_exp:n_exp + 2 * d * cpad].view(torch.float32).cpu().numpy()
     assert rt.size == d * cpad
+    # then 256 bytes: the down weights' largest row sum of |w|, then zeros
+    tail = p_h[n_exp + 2 * d * cpad:].view(torch.float32).cpu().numpy()
+    assert tail.size == 64 and np.all(tail[1:] == 0)
+    rowsum = np.abs(orc.h2f(dn16.view(np.uint16)).astype(np.float64)).reshape(E, d, I).sum(axis=2).max()
+    assert abs(tail[0] - rowsum) <= 1e-5 * rowsum, (tail[0], rowsum)
     want = np.zeros((d // 16, cpad, 4, 4), np.float32)
     # w[c][16g + 4s + kk] -> want[g][c][kk][s]
     want[:, :E] = wr.cpu().numpy().reshape(E, d // 16, 4, 4).transpose(1, 0, 3, 2)
@@ -462,6 +467,59 @@ def test_layer_fp32_activations_reused_workspace_and_tiles(ctx):
     finally:
         ctx.set_tile_policy(api.Context.TILE_ADAPTIVE)
         ctx.set_hot_rows(256)
+
+
+@pytest.mark.parametrize("mag", [1e4, 1e-4])
+def test_layer_fp32_activations_large_down_rows(ctx, mag):
+    """With packed weights the slot-scaled mode keeps the expert rows in fp16,
+    multiplied by 2^-c where 2^c exceeds the down weights' largest row sum of
+    |w|, a bound the packing writes into the packed buffer's last 256 bytes
+    (checked here against numpy's float64 sums).  One expert's down row set
+    to 4.0 throughout (row sum 1024, where the others sum to about 4) must
+    not overflow: the output against the oracle's fp32-row mode, within the
+    slot-scaled tolerance, and the same call on HF-layout weights (fp32
+    rows) within it too."""
+    cfg = dict(name="big_row", rows=300, d=512, experts=16, topk=4, inter=256, shared=256, skew=False)
+    inp = inputs.make_inputs(ctx, cfg, seed=31)
+    shape = inp["shape"]
+    T, d = shape["rows"], shape["d"]
+    inp["w_down"][3, 7, :] = 4.0
+    packed = ctx.pack_weights(shape, inp["w_router"], inp["w_gate_up"], inp["w_down"], inp["w_sh_gate_up"],
+                              inp["w_sh_down"])
+    ctx.sync()
+    bound = packed.view(torch.uint8)[-256:-252].cpu().numpy().view(np.float32)[0]
+    wd = np.abs(inp["w_down"].float().cpu().numpy().astype(np.float64)).sum(axis=2).max()
+    ws_ = np.abs(inp["w_sh_down"].float().cpu().numpy().astype(np.float64)).sum(axis=1).max()
+    want_bound = max(wd, ws_)
+    assert want_bound == 1024.0
+    assert abs(float(bound) - want_bound) <= 1e-5 * want_bound, (bound, want_bound)
+    g = torch.Generator(device="cuda").manual_seed(31)
+    x32 = torch.randn(T, d, device="cuda", generator=g, dtype=torch.float32) * mag
+    host = inputs.to_host(inp)
+    host["x"] = None
+    host["x32"] = x32.cpu().numpy()
+    ref = orc.layer(host, tile=16, x_scale=1, hp_scale=1, threads=16)
+    want = ref["out"].astype(np.float64)
+    idx = ref["idx"].reshape(T, -1)
+    assert (idx == 3).any(), "expert 3 must be routed"
+    for layout in ("packed", "hf"):
+        ws = torch.full((api.workspace_bytes_x32(shape),), 255, dtype=torch.uint8, device="cuda")
+        h = torch.zeros(T, 1, d, dtype=torch.float32, device="cuda")
+        inj = torch.zeros(T, 1, dtype=torch.float32, device="cuda")
+        if layout == "packed":
+            ctx.layer(shape, None, inp["w_router"], inp["bias"], None, None, None, None, None, ws, packed=packed,
+                      h=h, inj=inj, inj_stride=1, inj_off=0, hc=1, x32=x32)
+        else:
+            ctx.layer(shape, None, inp["w_router"], inp["bias"], inp["w_gate_up"], inp["w_down"],
+                      inp["w_sh_gate_up"], inp["w_sh_down"], None, ws, h=h, inj=inj, inj_stride=1, inj_off=0, hc=1,
+                      x32=x32)
+        ctx.sync()
+        y = h[:, 0, :].cpu().numpy().astype(np.float64)
+        assert np.isfinite(y).all(), layout
+        err = np.abs(y - want).max()
+        rel = np.linalg.norm(y - want) / np.linalg.norm(want)
+        print("  %s max|y| %.3g rel-L2 %.3g max-abs %.3g" % (layout, np.abs(want).max(), rel, err), flush=True)
+        assert rel <= 1e-3 and err <= 1e-2 * np.abs(want).max(), (layout, rel, err)
 
 
 def test_layer_fp32_activations_rejections(ctx):
