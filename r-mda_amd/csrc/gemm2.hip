@@ -1233,8 +1233,9 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
     // persistent: one workgroup per CU, a multiple of the 8 XCDs
     const uint32_t wgs = c.grid >= 8 ? c.grid / 8 * 8 : 8;
     const dim3 grid(wgs);
-    // the slot-scaled mode (fp32 SwiGLU output or fp32 rows) has its own
-    // instantiations, of the default configurations only
+    // the slot-scaled mode (fp32 SwiGLU output; fp32 rows, or fp16 rows under
+    // the weights' bound) has its own instantiations, of the default
+    // configurations only
     const bool sc = a->hp32 != nullptr || a->ye32 != nullptr || a->ye_bound != nullptr;
     if (sc) {
         if ((MODE == RMDA_GEMM_SWIGLU) != (a->hp32 != nullptr) ||
