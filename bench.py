@@ -66,7 +66,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=140)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", type=int, default=3, help="BASELINE configuration (1-5)")
+    ap.add_argument("--config", type=int, default=3, choices=range(1, 7),
+                    help="BASELINE configuration (1-5), or 6: the reference teacher's own MoE shape")
     ap.add_argument("--cpu-tokens", type=int, default=None,
                     help="tokens in the CPU-baseline sample (default: sized for ~10-30 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -703,7 +704,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
-    cfg = configs.CONFIGS[args.config]
+    cfg = configs.CONFIGS[args.config] if args.config in configs.CONFIGS else configs.TEACHER
     ctx = api.Context(0)
     inp = inputs.make_inputs(ctx, cfg, seed=0)
     shape = inp["shape"]
@@ -871,7 +872,7 @@ def main():
     if not args.no_cpu_baseline:
         n_tok = args.cpu_tokens
         if n_tok is None:
-            n_tok = {1: 256, 2: 128, 3: 512, 4: 512, 5: 256}[args.config]
+            n_tok = {1: 256, 2: 128, 3: 512, 4: 512, 5: 256, 6: 128}[args.config]
         cpu = cpu_baseline(inp, cfg, n_tok)
 
     if args.stages:
@@ -892,7 +893,7 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (counter-hash N(0,1) activations, N(0,0.02) weights, seed 0)",
-        "config": {"workload": workload_name(cfg, shape, args.config),
+        "config": {"workload": workload_name(cfg, shape, args.config if args.config in configs.CONFIGS else None),
                    "tokens": T, "d": shape["d"], "experts": shape["experts"], "topk": shape["topk"],
                    "inter": shape["inter"], "shared": shape["shared"], "parallelism": "single GPU"},
         "wall_ms_per_step": round(1000.0 * wall / args.steps, 5),
