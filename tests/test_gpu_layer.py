@@ -137,6 +137,16 @@ def test_layer_large(ctx, cfg):
     check_layer(ctx, cfg, seed=7)
 
 
+def test_layer_teacher_chunk_2048(ctx):
+    """The teacher's shape at a 2048-token chunk: with packed weights the
+    router's wide tile (32-token workgroups) takes the 512 experts' columns
+    and the route kernel the shared gate's; every logit bit-exact against the
+    oracle and bitwise equal to the HF-layout call (whose router computes the
+    gate itself), routing bit-exact, output within tolerance on sampled
+    rows."""
+    check_layer(ctx, dict(TEACHER, rows=2048, name="teacher_2048"), seed=5, n_sample=192)
+
+
 def test_layer_other_seed_and_ragged(ctx):
     cfg = dict(configs.CONFIGS[1], rows=203, name="ragged")
     check_layer(ctx, cfg, seed=5)
@@ -341,7 +351,10 @@ def test_layer_route_in_rank(ctx, cfg):
     (dict(name="shared_small", rows=300, d=512, experts=16, topk=4, inter=256, shared=256, skew=False), 1e6, None),
     (configs.CONFIGS[3], 1e6, 256),
     (configs.CONFIGS[4], 1e-6, 256),
-], ids=["tiny_1", "tiny_1e6", "tiny_1e-6", "shared_1e6", "prefill_1e6", "skewed_1e-6"])
+    # 512 experts + shared gate at 4096 tokens: the router's wide tile takes the
+    # experts' columns and the route kernel the shared gate's
+    (configs.CONFIGS[5], 1e-3, 128),
+], ids=["tiny_1", "tiny_1e6", "tiny_1e-6", "shared_1e6", "prefill_1e6", "skewed_1e-6", "fine_shared_1e-3"])
 def test_layer_fp32_activations(ctx, cfg, mag, n_sample):
     """rmda_moe_layer_args_t::x32: fp32 activations of magnitude 1e-6 .. 1e6
     (x32 = mag * N(0, 1), values not representable in fp16), through the
