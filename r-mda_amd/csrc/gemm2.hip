@@ -564,7 +564,7 @@ __device__ __forceinline__ task_desc_t task_desc(const task_sched_t &sched, cons
 // their ye tile with device-scope stores, wait for them, take one from the
 // arrival counter of each stored row's (token, 64 columns), and the wave that
 // takes a counter's last one sums that token's rows for its 64 columns.
-template <int MODE, int STAGES, int BPOL, int NDW, bool DB, bool FC = false, bool SC = false>
+template <int MODE, int STAGES, int BPOL, int NDW, bool DB, bool FC = false, bool SC = false, bool YNT = false>
 __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t BN = 256;
     constexpr uint32_t BK = 32;
@@ -810,7 +810,8 @@ __global__ __launch_bounds__(1024) void gemm3_kernel(rmda_gemm_args_t g) {
                                     __hip_atomic_store(dst, rmda_f2h(acc[i][j][v] * yinv), __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
                                 } else {
-                                    down_store<SC>(g, O, (size_t)(c_row0 + rr) * g.ldo + col, acc[i][j][v] * yinv);
+                                    down_store<SC, YNT>(g, O, (size_t)(c_row0 + rr) * g.ldo + col,
+                                                        acc[i][j][v] * yinv);
                                 }
                             }
                         }
@@ -1250,6 +1251,9 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
         }
         if (c.spec == 7 && MODE == RMDA_GEMM_SWIGLU && a->k % 64 == 0) {
             hipLaunchKernelGGL((gemm4_kernel<5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
+        } else if (c.spec != 4 && MODE == RMDA_GEMM_F16 && a->ye_nt != 0) {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true, false, true, true>), grid, dim3(16 * RMDA_WAVE), 0,
+                               s, *a);
         } else if (c.spec != 4) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true, false, true>), grid, dim3(16 * RMDA_WAVE), 0, s,
                                *a);
@@ -1272,7 +1276,10 @@ hipError_t launch_mode(hipStream_t s, const rmda_gemm_args_t *a, const rmda_gemm
                                s, *a);
             return hipGetLastError();
         }
-        if (c.spec != 4) {
+        if (c.spec != 4 && MODE == RMDA_GEMM_F16 && a->ye_nt != 0) {
+            hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true, false, false, true>), grid, dim3(16 * RMDA_WAVE), 0,
+                               s, *a);
+        } else if (c.spec != 4) {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, true>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);
         } else {
             hipLaunchKernelGGL((gemm3_kernel<MODE, 5, 2, 4, false>), grid, dim3(16 * RMDA_WAVE), 0, s, *a);

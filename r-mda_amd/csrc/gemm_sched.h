@@ -168,11 +168,16 @@ __device__ __forceinline__ float down_mul(const rmda_gemm_args_t &g) {
 }
 
 // One output of the down epilogue, already multiplied by down_mul: fp16
-// into ye, or fp32 into ye32 in the slot-scaled mode's fp32-row variant.
-template <bool SC>
+// into ye (non-temporal with NT: a compile-time choice, since a runtime
+// branch between two stores of the same value to the same address is
+// folded into one plain store), or fp32 into ye32 in the slot-scaled mode's
+// fp32-row variant.
+template <bool SC, bool NT = false>
 __device__ __forceinline__ void down_store(const rmda_gemm_args_t &g, uint16_t *O, size_t i, float y) {
     if (SC && g.ye32 != nullptr) {
         g.ye32[i] = y;
+    } else if constexpr (NT) {
+        __builtin_nontemporal_store(rmda_f2h(y), &O[i]);
     } else {
         O[i] = rmda_f2h(y);
     }
