@@ -990,7 +990,6 @@ static int gemm_pair(rmda_moe_ctx_t *ctx, hipStream_t s, rmda_gemm_args_t g, rmd
         rmda_gemm_args_t h = g;
         h.n_items = n_items_hot;
         h.fc = rmda_fc_t{};  // the compute tile leaves the combine to combine16_kernel
-        h.ye_nt = 0;         // and keeps ordinary stores
         const int rc = hip_check(ctx, rmda_launch_gemm_hot(s, &h, cfg.grid, ctx->hot_stages, ctx->hot_sched), what);
         if (rc != RMDA_OK || tile_mode == 2u) {
             return rc;
@@ -1272,12 +1271,12 @@ int rmda_moe_layer(rmda_moe_ctx_t *ctx, const rmda_moe_shape_t *shape, const rmd
         g.yscale = hslot;
         g.ye32 = x32 && packed == nullptr ? at<float>(ws, p.ye) : nullptr;
         g.ye_bound = x32 && packed != nullptr ? ye_bound : nullptr;
-        // experts averaging 64 rows or more: the streaming tile writes its
-        // fp16 rows with non-temporal stores.  Same-box A/B: config 3 layer
-        // -1.2 to -1.5% (down 93.6 -> 85.2 us, the combine, which then reads
-        // them from HBM, 10.0 -> 12.9), config 5 (80 rows) -0.6 to -0.7%; at
-        // 40 rows (the teacher's shape) +0.35% and at 8 (decode) +1.7%,
-        // hence the bound
+        // experts averaging 64 rows or more: either tile writes its fp16
+        // rows with non-temporal stores.  Same-box A/B: config 3 layer -1.2
+        // to -1.5% (down 93.6 -> 85.2 us, the combine, which then reads them
+        // from HBM, 10.0 -> 12.9), config 4 (compute tile) -1.8%, config 5
+        // (80 rows) -0.6 to -0.7%; at 40 rows (the teacher's shape) +0.35%
+        // and at 8 (decode) +1.7%, hence the bound
         g.ye_nt = p.npairs >= 64ull * E ? 1u : 0u;
         g.lda = I;
         g.w = w_dn;

@@ -511,8 +511,8 @@ struct rmda_gemm_args_t {
     const uint32_t *yscale;
     float *ye32;
     const uint32_t *ye_bound;
-    // F16, fp16 rows, packed weights: non-zero asks the streaming tile to
-    // store them with non-temporal stores
+    // F16, fp16 rows, packed weights: non-zero asks for non-temporal row
+    // stores (both tiles' default configurations)
     uint32_t ye_nt;
 };
 hipError_t rmda_launch_gemm(hipStream_t s, const rmda_gemm_args_t *a);

@@ -41,7 +41,7 @@ constexpr uint32_t HN = 256;               // N tile = one packed slab
 constexpr uint32_t HK = 32;                // K step
 constexpr uint32_t NW = 8;                 // waves
 
-template <int MODE, int STAGES, typename SCHED, bool PP, int BPOL, bool SC = false>
+template <int MODE, int STAGES, typename SCHED, bool PP, int BPOL, bool SC = false, bool YNT = false>
 __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
     constexpr uint32_t CH = HK / 8;                  // 16-byte chunks per row
     constexpr uint32_t RPI = 64 / CH;                // rows per DMA instruction
@@ -223,7 +223,8 @@ __global__ __launch_bounds__(512) void hot_gemm_kernel(rmda_gemm_args_t g) {
 #pragma unroll
                             for (int j = 0; j < 4; j += 1) {
                                 const uint32_t col = c_nt * HN + wn * 64 + j * 16 + fr;
-                                down_store<SC>(g, O, (size_t)(c_row0 + rr) * g.ldo + col, acc[i][j][v] * yinv);
+                                down_store<SC, YNT>(g, O, (size_t)(c_row0 + rr) * g.ldo + col,
+                                                    acc[i][j][v] * yinv);
                             }
                         }
                     }
@@ -383,10 +384,19 @@ hipError_t rmda_launch_gemm_hot(hipStream_t s, const rmda_gemm_args_t *a, uint32
         if (a->mode == RMDA_GEMM_SWIGLU) {
             hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_SWIGLU, 4, task_sched_t, true, 0, true>), gr,
                                dim3(NW * RMDA_WAVE), 0, s, *a);
+        } else if (a->ye_nt != 0) {
+            hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_F16, 4, task_sched_t, true, 0, true, true>), gr,
+                               dim3(NW * RMDA_WAVE), 0, s, *a);
         } else {
             hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_F16, 4, task_sched_t, true, 0, true>), gr,
                                dim3(NW * RMDA_WAVE), 0, s, *a);
         }
+        return hipGetLastError();
+    }
+    if (a->mode == RMDA_GEMM_F16 && a->ye_nt != 0 && stages == 4 && sched == 0) {
+        // the default configuration with non-temporal row stores
+        hipLaunchKernelGGL((hot_gemm_kernel<RMDA_GEMM_F16, 4, task_sched_t, true, 0, false, true>), gr,
+                           dim3(NW * RMDA_WAVE), 0, s, *a);
         return hipGetLastError();
     }
     if (a->mode == RMDA_GEMM_SWIGLU) {
