@@ -132,6 +132,14 @@ __global__ __launch_bounds__(256) void combine32_kernel(rmda_pc_moe_combine_t pc
     }
 }
 
+// One 16-byte slice of an expert row, read past the caches' normal retention:
+// every expert row is read by exactly one token's workgroup, once.
+typedef unsigned int rmda_u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 rmda_stream_load16(const uint4 *p) {
+    const rmda_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const rmda_u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // HC: the hyper-connection epilogue of shader/moe_combine.comp:36-38 in place
 // of (or besides) the fp16 output: h[r][s][c] += acc * 2 * sigmoid(inj / hc).
 template <bool HC>
@@ -181,11 +189,11 @@ __global__ __launch_bounds__(256) void combine16_kernel(const float *__restrict_
             if (s == RMDA_NONE) {
                 continue;
             }
-            rmda_comb_acc8(acc, s_wt[j], reinterpret_cast<const uint4 *>(y + (size_t)s * d)[c]);
+            rmda_comb_acc8(acc, s_wt[j], rmda_stream_load16(reinterpret_cast<const uint4 *>(y + (size_t)s * d) + c));
         }
         if (has_shared) {
             rmda_comb_acc8(acc, s_wt[RMDA_MAX_TOPK],
-                           reinterpret_cast<const uint4 *>(y + (size_t)s_slot[RMDA_MAX_TOPK] * d)[c]);
+                           rmda_stream_load16(reinterpret_cast<const uint4 *>(y + (size_t)s_slot[RMDA_MAX_TOPK] * d) + c));
         }
         if (out != nullptr) {
             reinterpret_cast<uint4 *>(out + (size_t)r * d)[c] = rmda_pack8_f16(acc);
